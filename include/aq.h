@@ -1,0 +1,59 @@
+/* aq: MI355X (gfx950) weight-quantized matmul kernels behind a plain C ABI.
+ *
+ * Every entry point takes caller-owned device pointers, shape scalars and a hipStream_t (passed as void*, so this
+ * header needs no HIP include), enqueues its kernels on that stream without synchronising, allocates nothing and
+ * returns an aq_status. Layouts are the reference's packed layouts:
+ *   Q4W  wq uint32 [N, K/8]: element k of row n in bits 4*(k%8) of word k/8, 4-bit two's complement
+ *        (value ((nib ^ 8) - 8) * ws[n, k/G]); ws fp16 [N, K/G].
+ *   T2W  w uint32 [K/16, N] (transposed): code of (n, k) in bits 2*(k%16) of word (k/16)*N + n, value
+ *        (code - 1) * s[k/128, n]; s fp16 [K/128, N].
+ *   X2H  uint32 [K/2]: fp16 pairs, the even k in the low half.
+ * fp16 values are passed as uint16_t bit patterns. Reference citations are file:line in adityaGoCT/mojo-adreno.
+ */
+#ifndef AQ_H
+#define AQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  AQ_OK = 0,
+  AQ_ERR_SHAPE = 1,    /* a size is zero/negative, or not a multiple the layout requires */
+  AQ_ERR_GROUP = 2,    /* group size not a multiple of 8, or K not a multiple of it */
+  AQ_ERR_ALIGN = 3,    /* a pointer is not 16-byte aligned */
+  AQ_ERR_LAUNCH = 4,   /* the HIP launch failed (hipGetLastError) */
+  AQ_ERR_NULL = 5,     /* a required pointer is NULL */
+  AQ_ERR_CAPACITY = 6, /* a size exceeds what the kernel's on-chip staging holds */
+  AQ_ERR_ARG = 7       /* any other invalid argument */
+} aq_status;
+
+/* Human-readable text of a status code (static storage). */
+const char* aq_status_string(int status);
+
+/* Library version, as major*10000 + minor*100 + patch. */
+int aq_version(void);
+
+/* ---- int4 (Q4W) matrix-vector products, decode ------------------------------------------------------------------
+ * y[t, n] = (add ? y[t, n] : 0) + sum_k W[n, k] * x[t, k] for t < tokens, fp32 x [tokens, K] and y [tokens, N].
+ * tokens = 1 is the decode GEMV; tokens <= 8 the few-token form. Every weight word is read once per launch for
+ * all tokens.
+ * Replaces: gemv_q4 (llama/kernels/gemv_q4.mojo:13-30, G=64), gemv_add_q4 (llama/kernels/gemv_add_q4.mojo:13-30,
+ * add=1), lk.gemv_q4[B] (lfm2/kernels/lk.mojo:134-143, G=32), moek.p_gemv_q4 / t_gemv_q4
+ * (qwen3moe/kernels/moek.mojo:273-281,528-545: tokens, add).
+ * Requires K % 32 == 0, K % group == 0, group % 8 == 0, tokens in 1..8, K*tokens <= 32768, 16-byte aligned wq/x. */
+int aq_gemv_q4(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int64_t n, int64_t k,
+               int32_t group, int32_t tokens, int32_t add, void* stream);
+
+/* a[t, j] = silu(W[j] . x[t]) * (W[f + j] . x[t]) for j < f over the fused gate|up matrix W [2f, K].
+ * Replaces: lk.gate_up_q4[B] (lfm2/kernels/lk.mojo:154-167). Same requirements as aq_gemv_q4. */
+int aq_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, float* a, int64_t f, int64_t k,
+                  int32_t group, int32_t tokens, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AQ_H */

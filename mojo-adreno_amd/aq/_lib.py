@@ -1,0 +1,62 @@
+"""ctypes binding of libaq.so, the C ABI declared in include/aq.h.
+
+The library is built in-tree (``mojo-adreno_amd/build.py``) and loaded from this directory. There is no fallback: if
+it is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("AQ_LIB", _HERE / "libaq.so"))
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+# name -> argument types (all return int status). Kept in the order of include/aq.h.
+SIGNATURES: dict[str, list] = {
+    "aq_version": [],
+    "aq_gemv_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p],
+    "aq_gate_up_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
+}
+
+_lib = None
+
+
+class AqError(RuntimeError):
+    """A non-zero aq_status from the C ABI."""
+
+    def __init__(self, fn: str, status: int):
+        self.status = status
+        super().__init__(f"{fn}: {status_string(status)} (status {status})")
+
+
+def lib() -> ctypes.CDLL:
+    """Load libaq.so once (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python mojo-adreno_amd/build.py`")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, args in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        handle.aq_status_string.argtypes = [ctypes.c_int]
+        handle.aq_status_string.restype = ctypes.c_char_p
+        _lib = handle
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().aq_status_string(int(status)).decode()
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise AqError on a non-zero status."""
+    st = getattr(lib(), name)(*args)
+    if st != 0:
+        raise AqError(name, st)

@@ -1,0 +1,77 @@
+"""CPU baseline for bench.py: the reference's own CPU path, restated. TEST/MEASUREMENT INFRASTRUCTURE ONLY.
+
+The reference checks this arithmetic on the CPU with PyTorch over *dequantised* weights: qwen3moe/reference.py:53-65
+dequantises the int4 words with numpy and runs fp32 torch layers (:121-129); llama/run.py:77-86,186-198 does the
+same for Llama. This module restates that path with torch on the host cores (fp32 ``F.linear`` over a dequantised
+matrix; dequantisation timed separately), so bench.py can report it beside the GPU numbers. Only bench.py's
+``cpu_baseline`` leg imports it.
+"""
+from __future__ import annotations
+
+import os
+import platform
+import time
+
+import numpy as np
+import torch
+
+
+def threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def dequant_q4(wq: np.ndarray, ws: np.ndarray, group: int) -> torch.Tensor:
+    """Q4W -> fp32 [N, K] as qwen3moe/reference.py:53-65 (``((nib ^ 8) - 8) * scale``), in torch on the CPU."""
+    w = torch.from_numpy(np.ascontiguousarray(wq).view(np.int32))
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
+    nib = (w.unsqueeze(-1) >> shifts) & 15
+    q = ((nib ^ 8) - 8).reshape(w.shape[0], -1).to(torch.float32)
+    s = torch.from_numpy(np.ascontiguousarray(ws).astype(np.float32))
+    return (q.reshape(w.shape[0], -1, group) * s.unsqueeze(-1)).reshape(q.shape)
+
+
+def median_time(fn, reps: int, budget_s: float) -> float:
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 3:
+            break
+    return float(np.median(times))
+
+
+def gemv_q4(wq, ws, x, group, reps=20, budget_s=4.0):
+    """Seconds for (matmul only, dequant + matmul) of one int4 GEMV, fp32."""
+    w = dequant_q4(wq, ws, group)
+    xt = torch.from_numpy(np.asarray(x, np.float32))
+    t_mm = median_time(lambda: torch.mv(w, xt), reps, budget_s / 2)
+    t_all = median_time(lambda: torch.mv(dequant_q4(wq, ws, group), xt), max(3, reps // 4), budget_s / 2)
+    return t_mm, t_all
+
+
+def gemm_layer(mats: dict, xs: dict, group: int, reps=5, budget_s=8.0):
+    """Seconds for one layer's projections ``F.linear(X, W_deq)`` in fp32 (matmul only), X fp32 copies of the fp16
+    activations."""
+    ws = {name: dequant_q4(q, s, group) for name, (q, s) in mats.items()}
+    xt = {k: torch.from_numpy(v.astype(np.float32)) for k, v in xs.items()}
+
+    def run():
+        for name, w in ws.items():
+            torch.nn.functional.linear(xt[w.shape[1]], w)
+
+    return median_time(run, reps, budget_s)

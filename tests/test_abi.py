@@ -1,0 +1,79 @@
+"""The C ABI library loads on a CPU-only host, exports every symbol include/aq.h declares, and rejects bad
+arguments before touching the GPU (no compute calls here)."""
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def _declared():
+    text = (ROOT / "include" / "aq.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(aq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    import aq
+    lib = aq.lib()
+    names = _declared()
+    assert "aq_gemv_q4" in names and len(names) >= 4
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared in include/aq.h but not exported: {missing}"
+
+
+def test_bindings_cover_every_declared_symbol():
+    from aq import _lib
+    names = set(_declared()) - {"aq_status_string"}
+    assert names <= set(_lib.SIGNATURES), f"no ctypes signature for {sorted(names - set(_lib.SIGNATURES))}"
+
+
+def test_status_strings():
+    from aq import _lib
+    assert _lib.status_string(0) == "ok"
+    assert "misaligned" in _lib.status_string(3)
+    assert "unknown" in _lib.status_string(999)
+
+
+def test_version():
+    import aq
+    assert aq.lib().aq_version() >= 100
+
+
+@pytest.mark.parametrize("args,status", [
+    ((None, None, None, None, 8, 512, 32, 1, 0, None), 5),  # NULL pointers
+])
+def test_gemv_rejects_null(args, status):
+    import aq
+    assert aq.lib().aq_gemv_q4(*args) == status
+
+
+def test_gemv_rejects_bad_shapes_before_launch():
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 500, 32, 1, 0, None) == 1      # K % 32 != 0
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 12, 1, 0, None) == 2      # group % 8 != 0
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 48, 1, 0, None) == 2      # K % group != 0
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 32, 9, 0, None) == 1      # tokens > 8
+    assert lib.aq_gemv_q4(p, p, p, p, 0, 512, 32, 1, 0, None) == 1      # N == 0
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 32768, 32, 2, 0, None) == 6    # x staging exceeds LDS
+    assert lib.aq_gemv_q4(p + 4, p, p, p, 8, 512, 32, 1, 0, None) == 3  # misaligned words
+    assert lib.aq_gate_up_q4(p, p, p, p, 8, 500, 32, 1, None) == 1
+
+
+def test_torch_ops_registered():
+    import torch
+    from aq import ops  # noqa: F401
+    for name in ("gemv_q4", "gate_up_q4"):
+        assert hasattr(torch.ops.aq, name)
+
+
+def test_ops_reject_host_tensors():
+    """No CPU fallback: host tensors are refused before any kernel call."""
+    import torch
+    from aq import ops
+    wq = torch.zeros((8, 64), dtype=torch.int32)
+    with pytest.raises((ValueError, NotImplementedError, RuntimeError)):
+        ops.gemv_q4(wq, torch.zeros((8, 16), dtype=torch.float16), torch.zeros(512), torch.zeros(8), 32)
