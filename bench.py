@@ -3,9 +3,13 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
-  value   C0 int4 decode GEMV (Llama-3.2-1B FFN up, 8192 x 2048, G = 32, fp32 x/y), GB/s of algorithmic bytes.
-          One step = one GEMV launch. The weights rotate over a pool of distinct copies (>= 512 MB, twice the
-          256 MB Infinity Cache), so every launch streams from HBM; the K timed steps are replayed from a hipGraph.
+  value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
+            (fused q|k|v 3072 x 2048, o 2048 x 2048, fused gate|up 16384 x 2048, down 2048 x 8192; G = 32), the
+            layer's weights rotating over 16 distinct layers (547 MB, more than the 256 MB Infinity Cache). FLOPs
+            count the true M (2 * 431 * 60.8 M weights = 52.4 GFLOP a step).
+  gemv_c0   C0 int4 decode GEMV (8192 x 2048, G = 32, fp32 x/y) GB/s over a rotating pool of >= 512 MB of distinct
+            weight copies: graph burst (time per launch) and single cold launch.
+The K timed steps are replayed from hipGraphs.
 Inputs are synthetic (seeded), resident in HBM before the timed region. ``--gpus N`` with N > 1 exits: this build
 measures one GPU.
 """
@@ -115,6 +119,70 @@ def bench_gemv_c0(dev, steps: int, warmup: int, pool_mb: int = 600):
                 pool_mb=round(copies * per / 1e6, 1), steps=len(seq))
 
 
+C1_LAYER = (("qkv", 3072, 2048), ("o", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192))
+
+
+def bench_gemm_c1(dev, steps: int, warmup: int, layers: int = 16):
+    """C1: one layer's four (fused) projection GEMMs a step, weights rotating over `layers` distinct layers."""
+    import numpy as np
+    import torch
+    from aq import ops, synth
+    m, g = synth.C1_TOKENS, 32
+    rng = np.random.default_rng(1)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(101)
+    xs = {k: _dev(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16), dev) for k in (2048, 8192)}
+    ys = {name: torch.empty((m, n), dtype=torch.float32, device=dev) for name, n, _ in C1_LAYER}
+    weights = []
+    for layer in range(layers):
+        lw = {}
+        for name, n, k in C1_LAYER:
+            if layer == 0:
+                wq, ws = synth.int4_matrix(rng, n, k, g)
+                lw[name] = (_dev(wq, dev), _dev(ws, dev))
+            else:
+                wq = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=gen)
+                ws = (torch.rand((n, k // g), device=dev, generator=gen) * 0.03 + 1e-3).to(torch.float16)
+                lw[name] = (wq, ws)
+        weights.append(lw)
+
+    def launch(layer, name):
+        k = dict((nm, kk) for nm, _, kk in C1_LAYER)[name]
+        wq, ws = weights[layer][name]
+        return lambda: ops.gemm_q4(xs[k], wq, ws, ys[name], g)
+
+    flop_step = sum(2 * m * n * k for _, n, k in C1_LAYER)
+    step_launches = [[launch(l, name) for name, _, _ in C1_LAYER] for l in range(layers)]
+    nsteps = max(steps, 1)
+    seq = [fn for i in range(nsteps) for fn in step_launches[i % layers]]
+    timer = GraphTimer(seq)
+    for _ in range(max(warmup, 1)):
+        timer.graph.replay()
+    torch.cuda.synchronize()
+    t_step = timer.time(replays=1) / nsteps
+    per = {}
+    for name, n, k in C1_LAYER:
+        tt = GraphTimer([launch(l, name) for l in range(layers)] * 2).time(replays=3) / (2 * layers)
+        per[name] = dict(us=round(tt * 1e6, 3), tflops=round(2 * m * n * k / tt / 1e12, 2))
+    return dict(flop=flop_step, t_step=t_step, steps=nsteps, per_gemm=per, layers=layers,
+                weights_mb=round(layers * sum(n * k * 0.5625 for _, n, k in C1_LAYER) / 1e6, 1))
+
+
+def cpu_baseline_gemm():
+    import numpy as np
+    from aq import synth
+    from oracle import cpu_baseline as cb
+    cores = cb.threads()
+    rng = np.random.default_rng(1)
+    mats = {name: synth.int4_matrix(rng, n, k, 32) for name, n, k in C1_LAYER}
+    xs = {k: rng.standard_normal((synth.C1_TOKENS, k), dtype=np.float32).astype(np.float16) for k in (2048, 8192)}
+    t = cb.gemm_layer(mats, xs, 32)
+    flop = sum(2 * synth.C1_TOKENS * n * k for _, n, k in C1_LAYER)
+    return dict(value=round(flop / t / 1e12, 4), unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"C1 one layer (4 fused projections, M=431, 52.4 GFLOP): torch fp32 F.linear over dequantised "
+                       f"weights, median of <=5 reps on {cb.cpu_model()}")
+
+
 def cpu_baseline_gemv():
     from aq import synth
     from oracle import cpu_baseline as cb
@@ -130,7 +198,7 @@ def cpu_baseline_gemv():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
     args = ap.parse_args()
@@ -145,25 +213,31 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    r = bench_gemv_c0(dev, args.steps, args.warmup)
+    c1 = bench_gemm_c1(dev, args.steps, args.warmup)
     wall = time.perf_counter() - t0
-    value = r["bytes"] / r["t_step"] / 1e9
+    r = bench_gemv_c0(dev, 128, 10)
+    value = c1["flop"] / c1["t_step"] / 1e12
+    gemv = r["bytes"] / r["t_burst"] / 1e9
     out = {
         "metric": "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
-        "ms_per_step": round(r["t_step"] * 1e3, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4xf32", "data": "synthetic",
-        "config": {"workload": "C0 int4 decode GEMV, Llama-3.2-1B FFN up 8192x2048, G=32, fp32 x/y",
-                   "pool_mb": r["pool_mb"], "rotating_copies": r["pool_copies"]},
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
-        "gemv_c0": {"gbs_graph_burst": round(r["bytes"] / r["t_burst"] / 1e9, 2),
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": c1["steps"], "warmup": args.warmup,
+        "ms_per_step": round(c1["t_step"] * 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4xf16->f32", "data": "synthetic",
+        "config": {"workload": "C1 int4 prefill GEMM: Llama-3.2-1B layer projections (q|k|v, o, gate|up, down) at "
+                               "M=431, fp16 activations, G=32, weights rotating over 16 layers",
+                   "tokens": 431, "weights_mb": c1["weights_mb"]},
+        "roofline": {"bound": "mfma", "achieved": round(value, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(value / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+        "gemm_c1_per_projection": c1["per_gemm"],
+        "gemv_c0": {"gbs_graph_burst": round(gemv, 2), "frac_hbm": round(gemv / HBM_PEAK_GBS, 4),
                     "gbs_single_cold": round(r["bytes"] / r["t_cold"] / 1e9, 2),
-                    "us_burst": round(r["t_burst"] * 1e6, 3), "us_single_cold": round(r["t_cold"] * 1e6, 3)},
+                    "us_burst": round(r["t_burst"] * 1e6, 3), "us_single_cold": round(r["t_cold"] * 1e6, 3),
+                    "pool_mb": r["pool_mb"]},
         "wall_s": round(wall, 2),
     }
     if not args.skip_cpu:
-        out["cpu_baseline"] = cpu_baseline_gemv()
+        out["cpu_baseline"] = cpu_baseline_gemm()
+        out["gemv_c0"]["cpu_baseline"] = cpu_baseline_gemv()
     print(json.dumps(out), flush=True)
 
 

@@ -52,6 +52,23 @@ int aq_gemv_q4(const uint32_t* wq, const uint16_t* ws, const float* x, float* y,
 int aq_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, float* a, int64_t f, int64_t k,
                   int32_t group, int32_t tokens, void* stream);
 
+/* ---- int4 (Q4W) GEMM on MFMA, prefill ------------------------------------------------------------------------------
+ * Y[m, n] = (add ? Y[m, n] : 0) + sum_k X[m, k] * W[n, k] with X [M, K] fp16 (x_is_f32 = 0) or fp32 (x_is_f32 = 1,
+ * rounded to fp16 on staging), Y fp32 [M, N]; W dequantised to fp16, fp32 accumulation (rel 1e-2 bar).
+ * Replaces: p_gemm_q4 (llama/kernels/prefill/p_gemm_q4.mojo:106-142, G=64, fp32 X) and lk.gemm_q4
+ * (lfm2/kernels/lk.mojo:458-495, G=32). The reference needs M, N % 128 and K % 16; here any M, N >= 1 and
+ * K % 32 == 0, K % group == 0, group % 8 == 0, 16-byte aligned x/wq/y, each operand < 2 GiB.
+ * workspace: caller-owned device memory for split-K partials, aq_gemm_q4_workspace_bytes(m, n, k) bytes (16-byte
+ * aligned); NULL or smaller runs one pass over K (correct, fewer workgroups). Calls sharing a workspace must be
+ * ordered on one stream. */
+int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y, int64_t m,
+               int64_t n, int64_t k, int32_t group, int32_t add, void* workspace, int64_t workspace_bytes,
+               void* stream);
+
+/* Workspace bytes aq_gemm_q4 uses for this shape (0 when it runs without split-K). No counterpart in the reference
+ * (its kernels need no scratch). */
+int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
 #ifdef __cplusplus
 }
 #endif

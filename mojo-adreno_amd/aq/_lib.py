@@ -21,7 +21,10 @@ SIGNATURES: dict[str, list] = {
     "aq_version": [],
     "aq_gemv_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p],
     "aq_gate_up_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
+    "aq_gemm_q4": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p],
+    "aq_gemm_q4_workspace_bytes": [_i64, _i64, _i64],
 }
+RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64}
 
 _lib = None
 
@@ -44,7 +47,7 @@ def lib() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         handle.aq_status_string.argtypes = [ctypes.c_int]
         handle.aq_status_string.restype = ctypes.c_char_p
         _lib = handle

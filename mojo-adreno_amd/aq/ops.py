@@ -81,6 +81,49 @@ _LIB.impl("gemv_q4", _gemv_q4_impl, "CUDA")
 _LIB.impl("gate_up_q4", _gate_up_q4_impl, "CUDA")
 
 
+# ---- int4 GEMM (prefill, MFMA) ----------------------------------------------------------------------------------
+
+_LIB.define("gemm_q4(Tensor x, Tensor wq, Tensor ws, Tensor(a!) y, int group, bool add, Tensor(b!) workspace) -> ()")
+
+_WORKSPACE: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-device scratch tensor of at least ``nbytes`` (grown on demand, reused by later calls on that device)."""
+    key = (device.type, device.index)
+    t = _WORKSPACE.get(key)
+    if t is None or t.numel() < nbytes:
+        t = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = t
+    return t
+
+
+def _gemm_q4_impl(x, wq, ws, y, group, add, workspace):
+    _dev(x, wq, ws, y)
+    _u32(wq, "wq")
+    _f16bits(ws, "ws")
+    _check(x.dtype in (torch.float16, torch.float32), "x must be float16 or float32")
+    _check(y.dtype == torch.float32, "y must be float32")
+    n, kw = wq.shape
+    k = kw * 8
+    _check(x.dim() == 2 and x.shape[1] == k, "x must be [M, K]")
+    m = x.shape[0]
+    _check(tuple(y.shape) == (m, n), "y must be [M, N]")
+    _check(ws.numel() == n * (k // group) and k % group == 0, "ws must be [N, K/group]")
+    _dev(workspace)
+    _lib.call("aq_gemm_q4", _ptr(x), int(x.dtype == torch.float32), _ptr(wq), _ptr(ws), _ptr(y), m, n, k, group,
+              int(add), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(x))
+
+
+_LIB.impl("gemm_q4", _gemm_q4_impl, "CUDA")
+
+
+def gemm_q4(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, y: torch.Tensor, group: int, add: bool = False):
+    """``Y (+)= X . deq(W)^T`` on MFMA: X fp16/fp32 [M, K], Q4W ``wq [N, K/8]``, fp16 ``ws [N, K/group]``, Y fp32."""
+    need = _lib.lib().aq_gemm_q4_workspace_bytes(x.shape[0], wq.shape[0], wq.shape[1] * 8)
+    torch.ops.aq.gemm_q4(x, wq, ws, y, group, add, workspace(x.device, need))
+
+
 def gemv_q4(wq: torch.Tensor, ws: torch.Tensor, x: torch.Tensor, y: torch.Tensor, group: int, add: bool = False):
     """``y[t] (+)= deq(W) . x[t]`` for Q4W ``wq [N, K/8]``, fp16 ``ws [N, K/group]``, fp32 ``x [T, K]``, T <= 8."""
     torch.ops.aq.gemv_q4(wq, ws, x, y, group, add)

@@ -32,10 +32,15 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-u
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# Per-source device flags. The MFMA kernels keep their accumulators in ordinary VGPRs: with AGPR accumulators the
+# register allocator rotates them through copies every loop iteration.
+EXTRA = {"aq_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
     if src.suffix == ".hip":
-        cmd = [hipcc(), *DEVICE, *COMMON, "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc(), *DEVICE, *EXTRA.get(src.name, []), *COMMON, "-c", str(src), "-o", str(obj)]
     else:  # host-only C++ (format converters, status text): the system compiler, no device pass
         cmd = ["g++", *COMMON, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)

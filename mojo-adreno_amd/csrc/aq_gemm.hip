@@ -1,0 +1,392 @@
+// int4 (Q4W) prefill GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
+//
+// Y[M, N] (+)= X[M, K] . deq(W)^T, W in Q4W (uint32 [N, K/8], fp16 scale per `group` weights of a row), X fp16 or
+// fp32 [M, K] (fp32 is rounded to fp16 when staged), Y fp32 [M, N], accumulation in fp32. This is the arithmetic of
+// llama/kernels/prefill/p_gemm_q4.mojo:106-142 (G = 64) and lfm2/kernels/lk.mojo:458-495 (G = 32); the reference
+// dequantises W to fp32 in shared memory and multiplies fp32 cooperative matrices, this kernel dequantises to fp16 in
+// registers and multiplies on MFMA.
+//
+// Tiling. A 256-thread workgroup (4 waves) owns BM = 16*MB rows and BN = 4 * 16*NB columns; wave w owns the column
+// strip [16*NB*w, +16*NB) for all BM rows (accumulators MB x NB 16x16 tiles). K advances in super-steps of 128 = four
+// MFMA k-steps of 32, with k permuted inside a super-step so that each lane's B operand is one contiguous 16-byte
+// load: lane l (column l%16, block b = l/16) takes k = 32b + 8s + {0..7} at MFMA step s, i.e. exactly the four words
+// b*4 .. b*4+3 of its row. Each word is dequantised straight into the MFMA B fragment: nibbles t and t+4 of the word
+// become one half2 (1024 + (nib ^ 8), via mask and OR with 0x6400), minus 1032, times the fp16 scale. The A operand (X)
+// is staged once per workgroup in LDS in fragment order with the same k permutation (halves 0,4,1,5,2,6,3,7 of each
+// 8-chunk), so a fragment is one ds_read_b128 per lane; slots are XOR-swizzled to keep staging writes 2-way. LDS is
+// double-buffered: the next super-step's X and W are fetched into registers while this one is multiplied.
+#include "aq_common.h"
+
+namespace aq {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kSuper = 128;  // k per super-step
+
+// Swizzled LDS slot (16 bytes each) of the A fragment of (row-block mb, step s, lane l).
+__device__ __forceinline__ int a_slot(int mb, int s, int l) {
+  const int sw = s | (((l >> 4) & 1) << 2);
+  return (mb * 4 + s) * 64 + (l ^ sw);
+}
+
+// Natural 8 fp16 (as 4 dwords: pairs (0,1),(2,3),(4,5),(6,7)) -> permuted pairs (0,4),(1,5),(2,6),(3,7).
+__device__ __forceinline__ uint4 permute8(uint4 d) {
+  uint4 e;
+  e.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  e.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  e.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  e.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return e;
+}
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+}
+
+// One Q4W word -> MFMA B fragment (8 fp16 in the permuted k order) scaled by s2 = (scale, scale).
+__device__ __forceinline__ half8 dequant_word(uint32_t w, half2v s2) {
+  const uint32_t u = w ^ 0x88888888u;
+  const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+  half8 out;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t bits = ((u >> (4 * t)) & 0x000F000Fu) | 0x64006400u;
+    half2v h = __builtin_bit_cast(half2v, bits);
+    h = (h - bias) * s2;
+    out[2 * t] = h[0];
+    out[2 * t + 1] = h[1];
+  }
+  return out;
+}
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zero (no branch needed).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource used here: the load returns zero
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return half_bits_to_float(h);
+}
+
+// One workgroup computes the BM x (4*NW) tile `tile` over super-steps [ks0, ks1). With SPLIT it writes its fp32
+// partial to part[split][M][N]; otherwise to y (store or accumulate).
+template <int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT>
+__global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv, const uint32_t* __restrict__ wq,
+                                                    const uint16_t* __restrict__ ws, float* __restrict__ y,
+                                                    float* __restrict__ part, int M, int N, int K, int group,
+                                                    int mtiles, int ntiles, int splits, int sup_per_split) {
+  constexpr int BM = 16 * MB;
+  constexpr int NW = 16 * NB;       // columns per wave
+  constexpr int XCH = BM * 16;      // 16-byte X chunks per super-step (16 per row)
+  constexpr int XPT = (XCH + 255) / 256;
+  extern __shared__ uint4 lds[];    // 2 stages x MB*4*64 slots
+
+  // Tile order: ids are split into (xcd = id % 8, local = id / 8) when the grid is a multiple of 8, so each XCD
+  // works through a contiguous run; within a run the m-tiles of one (n-tile, split) are adjacent (they share W).
+  int id = blockIdx.x;
+  const int nblk = gridDim.x;
+  if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+  const int mt = id % mtiles;
+  const int rest = id / mtiles;
+  const int sp = rest % splits;
+  const int nt = rest / splits;
+  if (nt >= ntiles) return;
+  const int nsup = (K + kSuper - 1) / kSuper;
+  const int ks0 = sp * sup_per_split;
+  const int ks1 = min(nsup, ks0 + sup_per_split);
+  const int m0 = mt * BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw0 = nt * (4 * NW) + wave * NW;  // this wave's first column
+  const int kw = K >> 3;                       // words per W row
+  const int gpr = K / group;
+
+  const __amdgpu_buffer_rsrc_t xr_rsrc = make_rsrc(xv, (uint32_t)((size_t)M * K * (XF32 ? 4 : 2)));
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)N * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)((size_t)N * gpr * 2));
+
+  // ---- per-lane B source: NB columns (16 apart), words (k + 32b)/8 .. +3 ----
+  const int bcol = lane & 15;
+  const int bblk = lane >> 4;
+  uint32_t wrow_off[NB], srow_off[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = nw0 + nb * 16 + bcol;
+    wrow_off[nb] = n < N ? (uint32_t)n * kw * 4 : kOOB;  // columns past N read zeros; results are not stored
+    srow_off[nb] = n < N ? (uint32_t)n * gpr * 2 : kOOB;
+  }
+
+  auto load_b = [&](int ks, bool live, uint4 (&wv)[NB], float (&sc)[NB][G32 ? 1 : 4]) {
+    const int k = ks * kSuper + 32 * bblk;
+    const bool ok = live && k < K;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      wv[nb] = buf_load16(w_rsrc, ok ? wrow_off[nb] + (uint32_t)(k >> 3) * 4 : kOOB);
+      if constexpr (G32) {
+        sc[nb][0] = buf_load_half(s_rsrc, ok ? srow_off[nb] + (uint32_t)(k / group) * 2 : kOOB);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sc[nb][j] = buf_load_half(s_rsrc, ok ? srow_off[nb] + (uint32_t)((k + 8 * j) / group) * 2 : kOOB);
+      }
+    }
+  };
+
+  // ---- X staging: chunk c = t + 256 i: row r = c / 16, 8-k chunk kc = c % 16 (s = kc % 4, b = kc / 4) ----
+  auto load_x = [&](int ks, bool live, uint4 (&xr)[XPT], uint4 (&xr2)[XPT]) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c >> 4;
+      const int kc = c & 15;
+      const int m = m0 + r;
+      const int k = ks * kSuper + kc * 8;
+      const bool ok = live && (c < XCH) && m < M && k < K;
+      const uint32_t e = (uint32_t)m * K + k;  // element offset
+      if constexpr (XF32) {
+        xr[i] = buf_load16(xr_rsrc, ok ? e * 4 : kOOB);
+        xr2[i] = buf_load16(xr_rsrc, ok ? e * 4 + 16 : kOOB);
+      } else {
+        xr[i] = buf_load16(xr_rsrc, ok ? e * 2 : kOOB);
+      }
+    }
+  };
+  auto store_x = [&](int buf, const uint4 (&xr)[XPT], const uint4 (&xr2)[XPT]) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      if (XCH % 256 == 0 || c < XCH) {
+        const int r = c >> 4;
+        const int kc = c & 15;
+        uint4 d;
+        if constexpr (XF32) {
+          d.x = pack_half2(__uint_as_float(xr[i].x), __uint_as_float(xr[i].y));
+          d.y = pack_half2(__uint_as_float(xr[i].z), __uint_as_float(xr[i].w));
+          d.z = pack_half2(__uint_as_float(xr2[i].x), __uint_as_float(xr2[i].y));
+          d.w = pack_half2(__uint_as_float(xr2[i].z), __uint_as_float(xr2[i].w));
+        } else {
+          d = xr[i];
+        }
+        const int l = (kc >> 2) * 16 + (r & 15);
+        lds[buf * (MB * 256) + a_slot(r >> 4, kc & 3, l)] = permute8(d);
+      }
+    }
+  };
+
+  float4v acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  uint4 xr[XPT], xr2[XPT];
+  uint4 wv[NB];
+  float sc[NB][G32 ? 1 : 4];
+  load_x(ks0, ks0 < ks1, xr, xr2);
+  load_b(ks0, ks0 < ks1, wv, sc);
+  store_x(0, xr, xr2);
+  __syncthreads();
+
+  // The loop body is one basic block: on the last step the prefetch re-reads the current slice and its LDS store goes
+  // to the idle buffer, which nothing reads again.
+  for (int ks = ks0; ks < ks1; ++ks) {
+    const int buf = (ks - ks0) & 1;
+    uint4 wn[NB];
+    float sn[NB][G32 ? 1 : 4];
+    const int kn = ks + 1 < ks1 ? ks + 1 : ks;  // the last step re-fetches its own slice (in bounds, unused)
+    load_x(kn, true, xr, xr2);
+    load_b(kn, true, wn, sn);
+    const uint4* abase = lds + buf * (MB * 256);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 a[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a[mb] = __builtin_bit_cast(half8, abase[a_slot(mb, s, lane)]);
+      half8 bf[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t w = s == 0 ? wv[nb].x : s == 1 ? wv[nb].y : s == 2 ? wv[nb].z : wv[nb].w;
+        const _Float16 h = (_Float16)sc[nb][G32 ? 0 : s];
+        bf[nb] = dequant_word(w, half2v{h, h});
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+    }
+    store_x(buf ^ 1, xr, xr2);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      wv[nb] = wn[nb];
+#pragma unroll
+      for (int j = 0; j < (G32 ? 1 : 4); ++j) sc[nb][j] = sn[nb][j];
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows past M ----
+  float* out = SPLIT ? part + (size_t)sp * M * N : y;
+  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(out, (uint32_t)((size_t)M * N * 4));
+  const int rq = (lane >> 4) * 4;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = nw0 + nb * 16 + bcol;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + mb * 16 + rq + r;
+        const uint32_t off = n < N ? ((uint32_t)m * N + n) * 4 : kOOB;
+        float v = acc[mb][nb][r];
+        if constexpr (ADD && !SPLIT) v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+      }
+    }
+  }
+}
+
+// y[i] = (add ? y[i] : 0) + sum_{s < splits} part[s][i], summed in split order (deterministic).
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, float* __restrict__ y,
+                                                       int64_t count, int splits, int add) {
+  const int64_t n4 = count >> 2;
+  const float4* p4 = reinterpret_cast<const float4*>(part);
+  float4* y4 = reinterpret_cast<float4*>(y);
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    float4 acc = add ? y4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < splits; ++s) {
+      const float4 v = p4[(int64_t)s * n4 + i];
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    y4[i] = acc;
+  }
+  for (int64_t i = (n4 << 2) + blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+    float acc = add ? y[i] : 0.f;
+    for (int s = 0; s < splits; ++s) acc += part[(int64_t)s * count + i];
+    y[i] = acc;
+  }
+}
+
+struct GemmPlan {
+  int mb, mtiles, ntiles, splits, sup_per_split;
+};
+
+// Rows per tile: the fewest 16-row blocks that cover M with ceil(M / 112) tiles (431 -> 4 x 112; at most 7 blocks,
+// so the accumulators and operands of a wave stay in 256 VGPRs). Splits of K: enough workgroups to cover the 256
+// CUs, each split keeping >= 2 super-steps of 128.
+constexpr int kMaxMB = 7;
+static GemmPlan plan_gemm(int M, int N, int K) {
+  GemmPlan p;
+  const int blocks16 = (M + 15) / 16;
+  p.mtiles = (blocks16 + kMaxMB - 1) / kMaxMB;
+  p.mb = (blocks16 + p.mtiles - 1) / p.mtiles;
+  p.ntiles = (N + 255) / 256;
+  const int nsup = (K + kSuper - 1) / kSuper;
+  const int tiles = p.mtiles * p.ntiles;
+  int s = 1;
+  while (tiles * s * 2 <= 320 && nsup / (s * 2) >= 2) s *= 2;
+  p.sup_per_split = (nsup + s - 1) / s;
+  p.splits = (nsup + p.sup_per_split - 1) / p.sup_per_split;
+  return p;
+}
+
+static int64_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
+  return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
+
+template <int MB, bool G32, bool XF32, bool ADD, bool SPLIT>
+static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
+                       int K, int group, const GemmPlan& p, hipStream_t s) {
+  constexpr int NB = 4;
+  const size_t lds = 2 * (size_t)MB * 256 * 16;
+  auto kern = k_gemm_q4<MB, NB, G32, XF32, ADD, SPLIT>;
+  if (lds > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return AQ_ERR_CAPACITY;
+  }
+  int blocks = p.mtiles * p.ntiles * p.splits;
+  blocks = (blocks + 7) / 8 * 8;  // extra workgroups exit at once; a multiple of 8 enables the XCD mapping
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, x, wq, ws, y, part, M, N, K, group, p.mtiles, p.ntiles,
+                     p.splits, p.sup_per_split);
+  return launch_status();
+}
+
+template <bool G32, bool XF32, bool ADD, bool SPLIT>
+static int gemm_mb(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
+                   int K, int group, const GemmPlan& p, hipStream_t s) {
+  switch (p.mb) {
+    case 1: return launch_gemm<1, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 2: return launch_gemm<2, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 3: return launch_gemm<3, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 4: return launch_gemm<4, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 5: return launch_gemm<5, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 6: return launch_gemm<6, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    default: return launch_gemm<7, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+  }
+}
+
+template <bool G32, bool XF32>
+static int gemm_dispatch(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
+                         int K, int group, int add, const GemmPlan& p, hipStream_t s) {
+  if (p.splits > 1) {
+    int st = gemm_mb<G32, XF32, false, true>(x, wq, ws, y, part, M, N, K, group, p, s);
+    if (st != AQ_OK) return st;
+    const int64_t count = (int64_t)M * N;
+    int64_t blocks = (count / 4 + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, s, part, y, count, p.splits, add);
+    return launch_status();
+  }
+  return add ? gemm_mb<G32, XF32, true, false>(x, wq, ws, y, part, M, N, K, group, p, s)
+             : gemm_mb<G32, XF32, false, false>(x, wq, ws, y, part, M, N, K, group, p, s);
+}
+
+static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_t* ws, float* y, int64_t m,
+                      int64_t n, int64_t k, int32_t group, int32_t add, void* workspace, int64_t ws_bytes,
+                      void* stream) {
+  if (!x || !wq || !ws || !y) return AQ_ERR_NULL;
+  if (m <= 0 || n <= 0 || k <= 0 || k % 32) return AQ_ERR_SHAPE;
+  if (m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return AQ_ERR_SHAPE;
+  if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
+  // buffer offsets are 32-bit: each operand must stay under 2 GiB
+  if (m * k * (xf32 ? 4 : 2) >= ((int64_t)1 << 31) || n * k / 2 >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
+  if (!aligned(wq, 16) || !aligned(x, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int M = (int)m, N = (int)n, K = (int)k;
+  GemmPlan p = plan_gemm(M, N, K);
+  if (p.splits > 1 && (!workspace || ws_bytes < gemm_workspace_bytes(p, M, N) || !aligned(workspace, 16))) {
+    p.splits = 1;  // no (or too small a) workspace: one pass over K
+    p.sup_per_split = (K + kSuper - 1) / kSuper;
+  }
+  float* part = static_cast<float*>(workspace);
+  const bool g32 = group % 32 == 0;
+  if (xf32) return g32 ? gemm_dispatch<true, true>(x, wq, ws, y, part, M, N, K, group, add, p, s)
+                       : gemm_dispatch<false, true>(x, wq, ws, y, part, M, N, K, group, add, p, s);
+  return g32 ? gemm_dispatch<true, false>(x, wq, ws, y, part, M, N, K, group, add, p, s)
+             : gemm_dispatch<false, false>(x, wq, ws, y, part, M, N, K, group, add, p, s);
+}
+
+}  // namespace aq
+
+extern "C" int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y,
+                          int64_t m, int64_t n, int64_t k, int32_t group, int32_t add, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+  return aq::gemm_entry(x, x_is_f32, wq, ws, y, m, n, k, group, add, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return 0;
+  const aq::GemmPlan p = aq::plan_gemm((int)m, (int)n, (int)k);
+  return aq::gemm_workspace_bytes(p, (int)m, (int)n);
+}
