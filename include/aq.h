@@ -69,6 +69,44 @@ int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16
  * (its kernels need no scratch). */
 int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
+/* ---- ternary (T2W) GEMM on MFMA, prefill ----------------------------------------------------------------------------
+ * Y[m, n] = (add ? Y : 0) + sum_k X[m, k] * (code(k, n) - 1) * s[k/128, n], X fp16 or fp32 (rounded to fp16),
+ * T2W w [K/16, N], s fp16 [K/128, N], fp32 accumulation (rel 1e-2 bar). Requires K % 128 == 0.
+ * Replaces: p_gemm_t2 / p_gemm_t2v (bonsai/kernels/prefill.mojo:155-171,174-313; M, N % 128 there), and the
+ * per-shape tile table gemm_table.gemm_t2 (qwen3/gemm_table.mojo:9-57): one kernel plans its own tiles and split.
+ * workspace as for aq_gemm_q4, aq_gemm_t2_workspace_bytes(m, n, k) bytes. */
+int aq_gemm_t2(const void* x, int32_t x_is_f32, const uint32_t* w, const uint16_t* s, float* y, int64_t m, int64_t n,
+               int64_t k, int32_t add, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* ---- ternary (T2W) matrix-vector products, decode ---------------------------------------------------------------
+ * y[n] = sum_k (code(k, n) - 1) * s[k/128, n] * x[k], x as X2H fp16 pairs [K/2], T2W w [K/16, N], s fp16 [K/128, N],
+ * fp32 accumulation (the reference accumulates groups in fp16). Requires K % 128 == 0, 16-byte aligned w.
+ * Replaces: packed_linear + packed_reduce (bonsai/kernels/kernels.mojo:283-325,437-448) in one launch.
+ * workspace: aq_t2_gemv_workspace_bytes(n, k) bytes, zero-filled before its first use: its first 64 KiB hold
+ * per-column-tile arrival counters (every call leaves them at zero again), the rest split-K partials. Keep it for
+ * aq_t2_gemv only; calls sharing it must be ordered on one stream. NULL runs without splitting K. */
+int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int64_t n, int64_t k,
+               void* workspace, int64_t workspace_bytes, void* stream);
+int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);
+
+/* partials[g, n] = sum over k in [1024 g, 1024 g + 1024) of the products above, g < ceil(K/1024).
+ * Replaces: packed_linear (bonsai/kernels/kernels.mojo:283-325; its grid (ceil(N/64), ceil(K/1024))). */
+int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials, int64_t n,
+                        int64_t k, void* stream);
+
+/* y[n] = sum_{g < groups} partials[g, n], in g order. Replaces: packed_reduce (bonsai/kernels/kernels.mojo:437-448). */
+int aq_t2_packed_reduce(const float* partials, float* y, int64_t n, int32_t groups, void* stream);
+
+/* ---- X2H producers (fp32 -> fp16 pairs, round to nearest even; even k in the low half) ------------------------ */
+/* q[i] = pack(x[2i], x[2i+1]), count = number of floats. Replaces: pack_half (qwen3/kernels/qwen3k.mojo:45-48). */
+int aq_pack_half(const float* x, uint32_t* q, int64_t count, void* stream);
+/* q[row] = pack(x[row] * rsqrt(mean(x[row]^2) + eps) * w), rows of n. Replaces: rmsnorm_pack
+ * (qwen3/kernels/qwen3k.mojo:30-42, eps 1e-6, one row). */
+int aq_rmsnorm_pack(const float* x, const float* w, uint32_t* q, int64_t rows, int64_t n, float eps, void* stream);
+/* q[row] = pack(silu(gate) * up), gu rows = gate (n) | up (n). Replaces: swiglu_pack (qwen3/kernels/qwen3k.mojo:51-59). */
+int aq_swiglu_pack(const float* gu, uint32_t* q, int64_t rows, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,8 +23,18 @@ SIGNATURES: dict[str, list] = {
     "aq_gate_up_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "aq_gemm_q4": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p],
     "aq_gemm_q4_workspace_bytes": [_i64, _i64, _i64],
+    "aq_gemm_t2": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],
+    "aq_gemm_t2_workspace_bytes": [_i64, _i64, _i64],
+    "aq_t2_gemv": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p],
+    "aq_t2_gemv_workspace_bytes": [_i64, _i64],
+    "aq_t2_packed_linear": [_p, _p, _p, _p, _i64, _i64, _p],
+    "aq_t2_packed_reduce": [_p, _p, _i64, _i32, _p],
+    "aq_pack_half": [_p, _p, _i64, _p],
+    "aq_rmsnorm_pack": [_p, _p, _p, _i64, _i64, ctypes.c_float, _p],
+    "aq_swiglu_pack": [_p, _p, _i64, _i64, _p],
 }
-RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64}
+RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64, "aq_t2_gemv_workspace_bytes": ctypes.c_int64,
+            "aq_gemm_t2_workspace_bytes": ctypes.c_int64}
 
 _lib = None
 

@@ -88,12 +88,13 @@ _LIB.define("gemm_q4(Tensor x, Tensor wq, Tensor ws, Tensor(a!) y, int group, bo
 _WORKSPACE: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A per-device scratch tensor of at least ``nbytes`` (grown on demand, reused by later calls on that device)."""
-    key = (device.type, device.index)
+def workspace(device: torch.device, nbytes: int, purpose: str = "gemm") -> torch.Tensor:
+    """A per-(device, purpose) zero-filled scratch tensor of at least ``nbytes``, grown on demand and reused by later
+    calls. Ops that keep arrival counters in it leave them at zero after every call."""
+    key = (device.type, device.index, purpose)
     t = _WORKSPACE.get(key)
     if t is None or t.numel() < nbytes:
-        t = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        t = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = t
     return t
 
@@ -132,3 +133,141 @@ def gemv_q4(wq: torch.Tensor, ws: torch.Tensor, x: torch.Tensor, y: torch.Tensor
 def gate_up_q4(wq: torch.Tensor, ws: torch.Tensor, x: torch.Tensor, a: torch.Tensor, group: int):
     """``a[t, j] = silu(W[j] . x[t]) * (W[f + j] . x[t])`` over the fused gate|up Q4W matrix ``[2f, K/8]``."""
     torch.ops.aq.gate_up_q4(wq, ws, x, a, group)
+
+
+# ---- ternary (T2W) GEMV and X2H producers --------------------------------------------------------------------------
+
+_LIB.define("t2_gemv(Tensor x2h, Tensor w, Tensor s, Tensor(a!) y, Tensor(b!) workspace) -> ()")
+_LIB.define("t2_packed_linear(Tensor x2h, Tensor w, Tensor s, Tensor(a!) partials) -> ()")
+_LIB.define("t2_packed_reduce(Tensor partials, Tensor(a!) y) -> ()")
+_LIB.define("pack_half(Tensor x, Tensor(a!) q) -> ()")
+_LIB.define("rmsnorm_pack(Tensor x, Tensor w, Tensor(a!) q, float eps) -> ()")
+_LIB.define("swiglu_pack(Tensor gu, Tensor(a!) q) -> ()")
+
+
+def _t2_shapes(x2h, w, s):
+    _dev(x2h, w, s)
+    _u32(x2h, "x2h")
+    _u32(w, "w")
+    _f16bits(s, "s")
+    kw, n = w.shape
+    k = kw * 16
+    _check(x2h.numel() == k // 2, "x2h must hold K/2 fp16 pairs")
+    _check(tuple(s.shape) == (k // 128, n), "s must be [K/128, N]")
+    return n, k
+
+
+def _t2_gemv_impl(x2h, w, s, y, workspace):
+    n, k = _t2_shapes(x2h, w, s)
+    _dev(y, workspace)
+    _check(y.dtype == torch.float32 and y.numel() == n, "y must be float32 [N]")
+    _lib.call("aq_t2_gemv", _ptr(x2h), _ptr(w), _ptr(s), _ptr(y), n, k, _ptr(workspace),
+              workspace.numel() * workspace.element_size(), _stream(y))
+
+
+def _t2_packed_linear_impl(x2h, w, s, partials):
+    n, k = _t2_shapes(x2h, w, s)
+    _dev(partials)
+    _check(partials.dtype == torch.float32 and tuple(partials.shape) == ((k + 1023) // 1024, n),
+           "partials must be float32 [ceil(K/1024), N]")
+    _lib.call("aq_t2_packed_linear", _ptr(x2h), _ptr(w), _ptr(s), _ptr(partials), n, k, _stream(partials))
+
+
+def _t2_packed_reduce_impl(partials, y):
+    _dev(partials, y)
+    _check(partials.dtype == torch.float32 and y.dtype == torch.float32, "float32 tensors")
+    g, n = partials.shape
+    _check(y.numel() == n, "y must be [N]")
+    _lib.call("aq_t2_packed_reduce", _ptr(partials), _ptr(y), n, g, _stream(y))
+
+
+def _pack_half_impl(x, q):
+    _dev(x, q)
+    _check(x.dtype == torch.float32, "x must be float32")
+    _u32(q, "q")
+    _check(q.numel() * 2 == x.numel(), "q must hold numel(x)/2 words")
+    _lib.call("aq_pack_half", _ptr(x), _ptr(q), x.numel(), _stream(x))
+
+
+def _rmsnorm_pack_impl(x, w, q, eps):
+    _dev(x, w, q)
+    _check(x.dtype == torch.float32 and w.dtype == torch.float32, "x and w must be float32")
+    _u32(q, "q")
+    n = w.numel()
+    rows = x.numel() // n
+    _check(x.numel() == rows * n and q.numel() * 2 == x.numel(), "x [rows, n], q [rows, n/2]")
+    _lib.call("aq_rmsnorm_pack", _ptr(x), _ptr(w), _ptr(q), rows, n, float(eps), _stream(x))
+
+
+def _swiglu_pack_impl(gu, q):
+    _dev(gu, q)
+    _check(gu.dtype == torch.float32, "gu must be float32")
+    _u32(q, "q")
+    n2 = gu.shape[-1]
+    rows = gu.numel() // n2
+    _check(n2 % 4 == 0 and q.numel() == rows * n2 // 4, "gu [rows, 2n], q [rows, n/2]")
+    _lib.call("aq_swiglu_pack", _ptr(gu), _ptr(q), rows, n2 // 2, _stream(gu))
+
+
+_LIB.impl("t2_gemv", _t2_gemv_impl, "CUDA")
+_LIB.impl("t2_packed_linear", _t2_packed_linear_impl, "CUDA")
+_LIB.impl("t2_packed_reduce", _t2_packed_reduce_impl, "CUDA")
+_LIB.impl("pack_half", _pack_half_impl, "CUDA")
+_LIB.impl("rmsnorm_pack", _rmsnorm_pack_impl, "CUDA")
+_LIB.impl("swiglu_pack", _swiglu_pack_impl, "CUDA")
+
+
+def t2_gemv(x2h: torch.Tensor, w: torch.Tensor, s: torch.Tensor, y: torch.Tensor):
+    """``y = deq_T2(W) . x`` for T2W ``w [K/16, N]``, fp16 ``s [K/128, N]``, X2H ``x2h [K/2]``; y fp32 [N]."""
+    need = _lib.lib().aq_t2_gemv_workspace_bytes(w.shape[1], w.shape[0] * 16)
+    torch.ops.aq.t2_gemv(x2h, w, s, y, workspace(y.device, need, "t2_gemv"))
+
+
+def t2_packed_linear(x2h, w, s, partials):
+    torch.ops.aq.t2_packed_linear(x2h, w, s, partials)
+
+
+def t2_packed_reduce(partials, y):
+    torch.ops.aq.t2_packed_reduce(partials, y)
+
+
+def pack_half(x: torch.Tensor, q: torch.Tensor):
+    torch.ops.aq.pack_half(x, q)
+
+
+def rmsnorm_pack(x: torch.Tensor, w: torch.Tensor, q: torch.Tensor, eps: float = 1e-6):
+    torch.ops.aq.rmsnorm_pack(x, w, q, eps)
+
+
+def swiglu_pack(gu: torch.Tensor, q: torch.Tensor):
+    torch.ops.aq.swiglu_pack(gu, q)
+
+
+# ---- ternary (T2W) GEMM (prefill, MFMA) -----------------------------------------------------------------------------
+
+_LIB.define("gemm_t2(Tensor x, Tensor w, Tensor s, Tensor(a!) y, bool add, Tensor(b!) workspace) -> ()")
+
+
+def _gemm_t2_impl(x, w, s, y, add, workspace):
+    _dev(x, w, s, y, workspace)
+    _u32(w, "w")
+    _f16bits(s, "s")
+    _check(x.dtype in (torch.float16, torch.float32), "x must be float16 or float32")
+    _check(y.dtype == torch.float32, "y must be float32")
+    kw, n = w.shape
+    k = kw * 16
+    _check(x.dim() == 2 and x.shape[1] == k, "x must be [M, K]")
+    m = x.shape[0]
+    _check(tuple(y.shape) == (m, n), "y must be [M, N]")
+    _check(tuple(s.shape) == (k // 128, n), "s must be [K/128, N]")
+    _lib.call("aq_gemm_t2", _ptr(x), int(x.dtype == torch.float32), _ptr(w), _ptr(s), _ptr(y), m, n, k, int(add),
+              _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(x))
+
+
+_LIB.impl("gemm_t2", _gemm_t2_impl, "CUDA")
+
+
+def gemm_t2(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, y: torch.Tensor, add: bool = False):
+    """``Y (+)= X . deq_T2(W)^T`` on MFMA: X fp16/fp32 [M, K], T2W ``w [K/16, N]``, fp16 ``s [K/128, N]``, Y fp32."""
+    need = _lib.lib().aq_gemm_t2_workspace_bytes(x.shape[0], w.shape[1], w.shape[0] * 16)
+    torch.ops.aq.gemm_t2(x, w, s, y, add, workspace(x.device, need))

@@ -1,4 +1,4 @@
-// int4 (Q4W) prefill GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
+// int4 (Q4W) and ternary (T2W) prefill GEMMs on CDNA4 matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
 //
 // Y[M, N] (+)= X[M, K] . deq(W)^T, W in Q4W (uint32 [N, K/8], fp16 scale per `group` weights of a row), X fp16 or
 // fp32 [M, K] (fp32 is rounded to fp16 when staged), Y fp32 [M, N], accumulation in fp32. This is the arithmetic of
@@ -77,18 +77,27 @@ __device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_
   return half_bits_to_float(h);
 }
 
-// One workgroup computes the BM x (4*NW) tile `tile` over super-steps [ks0, ks1). With SPLIT it writes its fp32
-// partial to part[split][M][N]; otherwise to y (store or accumulate).
-template <int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT>
-__global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv, const uint32_t* __restrict__ wq,
-                                                    const uint16_t* __restrict__ ws, float* __restrict__ y,
-                                                    float* __restrict__ part, int M, int N, int K, int group,
-                                                    int mtiles, int ntiles, int splits, int sup_per_split) {
+enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transposed words [K/16, N]
+
+// One workgroup computes the BM x (4*NW) tile over super-steps [ks0, ks1). With SPLIT it writes its fp32 partial to
+// part[split][M][N]; otherwise to y (store or accumulate).
+//
+// T2W (FMT = kT2): lane (column n, block b) loads the two words (k-rows (k0 + 32b)/16 and +1) of its column; MFMA
+// step s takes word s/2, code positions j = 4(s%2) + t and j + 8 (t = 0..3) as fp16 pairs (1024 + c, via mask and
+// OR), minus 1025, times the column's fp16 scale for this 128-group. X is staged with the same pairing: 8-k chunks
+// A (k 0..7 of a 16-k word) and B (k 8..15) interleave as (A[4h+t], B[4h+t]).
+template <int FMT, int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT>
+__global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, const uint32_t* __restrict__ wq,
+                                                 const uint16_t* __restrict__ ws, float* __restrict__ y,
+                                                 float* __restrict__ part, int M, int N, int K, int group,
+                                                 int mtiles, int ntiles, int splits, int sup_per_split) {
   constexpr int BM = 16 * MB;
-  constexpr int NW = 16 * NB;       // columns per wave
-  constexpr int XCH = BM * 16;      // 16-byte X chunks per super-step (16 per row)
-  constexpr int XPT = (XCH + 255) / 256;
-  extern __shared__ uint4 lds[];    // 2 stages x MB*4*64 slots
+  constexpr int NW = 16 * NB;                      // columns per wave
+  constexpr int UPR = FMT == kT2 ? 8 : 16;          // staging units per row per super-step (16 or 8 k each)
+  constexpr int UNITS = BM * UPR;
+  constexpr int UPT = (UNITS + 255) / 256;          // units per thread
+  constexpr int UL = (FMT == kT2 ? 2 : 1) * (XF32 ? 2 : 1);  // 16-byte loads per unit
+  extern __shared__ uint4 lds[];                    // 2 stages x MB*4*64 fragment slots
 
   // Tile order: ids are split into (xcd = id % 8, local = id / 8) when the grid is a multiple of 8, so each XCD
   // works through a contiguous run; within a run the m-tiles of one (n-tile, split) are adjacent (they share W).
@@ -107,77 +116,127 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv,
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw0 = nt * (4 * NW) + wave * NW;  // this wave's first column
-  const int kw = K >> 3;                       // words per W row
+  const int kw = K >> 3;                       // Q4W words per row
   const int gpr = K / group;
 
   const __amdgpu_buffer_rsrc_t xr_rsrc = make_rsrc(xv, (uint32_t)((size_t)M * K * (XF32 ? 4 : 2)));
-  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)N * kw * 4));
-  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)((size_t)N * gpr * 2));
+  const __amdgpu_buffer_rsrc_t w_rsrc =
+      make_rsrc(wq, (uint32_t)(FMT == kT2 ? (size_t)(K >> 4) * N * 4 : (size_t)N * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc =
+      make_rsrc(ws, (uint32_t)(FMT == kT2 ? (size_t)(K >> 7) * N * 2 : (size_t)N * gpr * 2));
 
-  // ---- per-lane B source: NB columns (16 apart), words (k + 32b)/8 .. +3 ----
+  // ---- per-lane B source: NB columns (16 apart) ----
   const int bcol = lane & 15;
   const int bblk = lane >> 4;
-  uint32_t wrow_off[NB], srow_off[NB];
+  int ncol[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int n = nw0 + nb * 16 + bcol;
-    wrow_off[nb] = n < N ? (uint32_t)n * kw * 4 : kOOB;  // columns past N read zeros; results are not stored
-    srow_off[nb] = n < N ? (uint32_t)n * gpr * 2 : kOOB;
-  }
+  for (int nb = 0; nb < NB; ++nb) ncol[nb] = nw0 + nb * 16 + bcol;  // columns past N read zeros, are not stored
 
-  auto load_b = [&](int ks, bool live, uint4 (&wv)[NB], float (&sc)[NB][G32 ? 1 : 4]) {
+  auto load_b = [&](int ks, uint4 (&wv)[NB], float (&sc)[NB][G32 ? 1 : 4]) {
     const int k = ks * kSuper + 32 * bblk;
-    const bool ok = live && k < K;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      wv[nb] = buf_load16(w_rsrc, ok ? wrow_off[nb] + (uint32_t)(k >> 3) * 4 : kOOB);
-      if constexpr (G32) {
-        sc[nb][0] = buf_load_half(s_rsrc, ok ? srow_off[nb] + (uint32_t)(k / group) * 2 : kOOB);
+      const int n = ncol[nb];
+      const bool ok = k < K && n < N;
+      if constexpr (FMT == kT2) {
+        const uint32_t kr = (uint32_t)(k >> 4);
+        wv[nb].x = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, ok ? (kr * N + n) * 4 : kOOB, 0, 0);
+        wv[nb].y = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, ok ? ((kr + 1) * N + n) * 4 : kOOB, 0, 0);
+        wv[nb].z = wv[nb].w = 0;
+        sc[nb][0] = buf_load_half(s_rsrc, ok ? ((uint32_t)(k >> 7) * N + n) * 2 : kOOB);
       } else {
+        const uint32_t row = (uint32_t)n * kw * 4;
+        wv[nb] = buf_load16(w_rsrc, ok ? row + (uint32_t)(k >> 3) * 4 : kOOB);
+        if constexpr (G32) {
+          sc[nb][0] = buf_load_half(s_rsrc, ok ? (uint32_t)n * gpr * 2 + (uint32_t)(k / group) * 2 : kOOB);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sc[nb][j] = buf_load_half(s_rsrc, ok ? srow_off[nb] + (uint32_t)((k + 8 * j) / group) * 2 : kOOB);
+          for (int j = 0; j < 4; ++j)
+            sc[nb][j] = buf_load_half(s_rsrc, ok ? (uint32_t)n * gpr * 2 + (uint32_t)((k + 8 * j) / group) * 2
+                                                 : kOOB);
+        }
       }
     }
   };
 
-  // ---- X staging: chunk c = t + 256 i: row r = c / 16, 8-k chunk kc = c % 16 (s = kc % 4, b = kc / 4) ----
-  auto load_x = [&](int ks, bool live, uint4 (&xr)[XPT], uint4 (&xr2)[XPT]) {
+  // B fragment of MFMA step s for column block nb.
+  auto dequant = [&](int s, const uint4& w4, float scale) -> half8 {
+    const _Float16 h = (_Float16)scale;
+    const half2v s2 = {h, h};
+    if constexpr (FMT == kT2) {
+      const uint32_t w = s < 2 ? w4.x : w4.y;
+      const half2v bias = {(_Float16)1025.0f, (_Float16)1025.0f};
+      half8 out;
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int r = c >> 4;
-      const int kc = c & 15;
-      const int m = m0 + r;
-      const int k = ks * kSuper + kc * 8;
-      const bool ok = live && (c < XCH) && m < M && k < K;
-      const uint32_t e = (uint32_t)m * K + k;  // element offset
-      if constexpr (XF32) {
-        xr[i] = buf_load16(xr_rsrc, ok ? e * 4 : kOOB);
-        xr2[i] = buf_load16(xr_rsrc, ok ? e * 4 + 16 : kOOB);
-      } else {
-        xr[i] = buf_load16(xr_rsrc, ok ? e * 2 : kOOB);
+      for (int t = 0; t < 4; ++t) {
+        const int j = 4 * (s & 1) + t;
+        const uint32_t bits = ((w >> (2 * j)) & 0x00030003u) | 0x64006400u;
+        half2v v = (__builtin_bit_cast(half2v, bits) - bias) * s2;
+        out[2 * t] = v[0];
+        out[2 * t + 1] = v[1];
       }
+      return out;
+    } else {
+      const uint32_t w = s == 0 ? w4.x : s == 1 ? w4.y : s == 2 ? w4.z : w4.w;
+      return dequant_word(w, s2);
     }
   };
-  auto store_x = [&](int buf, const uint4 (&xr)[XPT], const uint4 (&xr2)[XPT]) {
+
+  // ---- X staging: unit u = t + 256 i: row r = u / UPR, k offset ku * (16 or 8) ----
+  auto load_x = [&](int ks, uint4 (&xr)[UPT][UL]) {
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      if (XCH % 256 == 0 || c < XCH) {
-        const int r = c >> 4;
-        const int kc = c & 15;
-        uint4 d;
-        if constexpr (XF32) {
-          d.x = pack_half2(__uint_as_float(xr[i].x), __uint_as_float(xr[i].y));
-          d.y = pack_half2(__uint_as_float(xr[i].z), __uint_as_float(xr[i].w));
-          d.z = pack_half2(__uint_as_float(xr2[i].x), __uint_as_float(xr2[i].y));
-          d.w = pack_half2(__uint_as_float(xr2[i].z), __uint_as_float(xr2[i].w));
-        } else {
-          d = xr[i];
+    for (int i = 0; i < UPT; ++i) {
+      const int u = threadIdx.x + 256 * i;
+      const int r = u / UPR;
+      const int ku = u % UPR;
+      const int m = m0 + r;
+      const int k = ks * kSuper + ku * (FMT == kT2 ? 16 : 8);
+      const bool ok = (UNITS % 256 == 0 || u < UNITS) && m < M && k < K;
+      const uint32_t e = ((uint32_t)m * K + k) * (XF32 ? 4 : 2);  // byte offset
+#pragma unroll
+      for (int q = 0; q < UL; ++q) xr[i][q] = buf_load16(xr_rsrc, ok ? e + 16 * q : kOOB);
+    }
+  };
+  auto store_x = [&](int buf, const uint4 (&xr)[UPT][UL]) {
+    uint4* base = lds + buf * (MB * 256);
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = threadIdx.x + 256 * i;
+      if (UNITS % 256 == 0 || u < UNITS) {
+        const int r = u / UPR;
+        const int ku = u % UPR;
+        uint4 c[FMT == kT2 ? 2 : 1];  // fp16 8-k chunks of this unit
+#pragma unroll
+        for (int q = 0; q < (FMT == kT2 ? 2 : 1); ++q) {
+          if constexpr (XF32) {
+            const uint4 a = xr[i][2 * q], b = xr[i][2 * q + 1];
+            c[q].x = pack_half2(__uint_as_float(a.x), __uint_as_float(a.y));
+            c[q].y = pack_half2(__uint_as_float(a.z), __uint_as_float(a.w));
+            c[q].z = pack_half2(__uint_as_float(b.x), __uint_as_float(b.y));
+            c[q].w = pack_half2(__uint_as_float(b.z), __uint_as_float(b.w));
+          } else {
+            c[q] = xr[i][q];
+          }
         }
-        const int l = (kc >> 2) * 16 + (r & 15);
-        lds[buf * (MB * 256) + a_slot(r >> 4, kc & 3, l)] = permute8(d);
+        if constexpr (FMT == kT2) {
+          const int l = (ku >> 1) * 16 + (r & 15);
+          const int s0 = 2 * (ku & 1);
+          const uint4 A = c[0], B = c[1];
+          uint4 f0, f1;
+          f0.x = __builtin_amdgcn_perm(B.x, A.x, 0x05040100u);
+          f0.y = __builtin_amdgcn_perm(B.x, A.x, 0x07060302u);
+          f0.z = __builtin_amdgcn_perm(B.y, A.y, 0x05040100u);
+          f0.w = __builtin_amdgcn_perm(B.y, A.y, 0x07060302u);
+          f1.x = __builtin_amdgcn_perm(B.z, A.z, 0x05040100u);
+          f1.y = __builtin_amdgcn_perm(B.z, A.z, 0x07060302u);
+          f1.z = __builtin_amdgcn_perm(B.w, A.w, 0x05040100u);
+          f1.w = __builtin_amdgcn_perm(B.w, A.w, 0x07060302u);
+          base[a_slot(r >> 4, s0, l)] = f0;
+          base[a_slot(r >> 4, s0 + 1, l)] = f1;
+        } else {
+          const int l = (ku >> 2) * 16 + (r & 15);
+          base[a_slot(r >> 4, ku & 3, l)] = permute8(c[0]);
+        }
       }
     }
   };
@@ -188,12 +247,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv,
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  uint4 xr[XPT], xr2[XPT];
+  uint4 xr[UPT][UL];
   uint4 wv[NB];
   float sc[NB][G32 ? 1 : 4];
-  load_x(ks0, ks0 < ks1, xr, xr2);
-  load_b(ks0, ks0 < ks1, wv, sc);
-  store_x(0, xr, xr2);
+  load_x(ks0, xr);
+  load_b(ks0, wv, sc);
+  store_x(0, xr);
   __syncthreads();
 
   // The loop body is one basic block: on the last step the prefetch re-reads the current slice and its LDS store goes
@@ -203,8 +262,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv,
     uint4 wn[NB];
     float sn[NB][G32 ? 1 : 4];
     const int kn = ks + 1 < ks1 ? ks + 1 : ks;  // the last step re-fetches its own slice (in bounds, unused)
-    load_x(kn, true, xr, xr2);
-    load_b(kn, true, wn, sn);
+    load_x(kn, xr);
+    load_b(kn, wn, sn);
     const uint4* abase = lds + buf * (MB * 256);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -213,18 +272,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(const void* __restrict__ xv,
       for (int mb = 0; mb < MB; ++mb) a[mb] = __builtin_bit_cast(half8, abase[a_slot(mb, s, lane)]);
       half8 bf[NB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint32_t w = s == 0 ? wv[nb].x : s == 1 ? wv[nb].y : s == 2 ? wv[nb].z : wv[nb].w;
-        const _Float16 h = (_Float16)sc[nb][G32 ? 0 : s];
-        bf[nb] = dequant_word(w, half2v{h, h});
-      }
+      for (int nb = 0; nb < NB; ++nb) bf[nb] = dequant(s, wv[nb], sc[nb][G32 ? 0 : s]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mb], bf[nb], acc[mb][nb], 0, 0, 0);
     }
-    store_x(buf ^ 1, xr, xr2);
+    store_x(buf ^ 1, xr);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       wv[nb] = wn[nb];
@@ -303,12 +358,12 @@ static int64_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
 }
 
-template <int MB, bool G32, bool XF32, bool ADD, bool SPLIT>
+template <int FMT, int MB, bool G32, bool XF32, bool ADD, bool SPLIT>
 static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
                        int K, int group, const GemmPlan& p, hipStream_t s) {
   constexpr int NB = 4;
   const size_t lds = 2 * (size_t)MB * 256 * 16;
-  auto kern = k_gemm_q4<MB, NB, G32, XF32, ADD, SPLIT>;
+  auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT>;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
@@ -321,25 +376,25 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
   return launch_status();
 }
 
-template <bool G32, bool XF32, bool ADD, bool SPLIT>
+template <int FMT, bool G32, bool XF32, bool ADD, bool SPLIT>
 static int gemm_mb(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
                    int K, int group, const GemmPlan& p, hipStream_t s) {
   switch (p.mb) {
-    case 1: return launch_gemm<1, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    case 2: return launch_gemm<2, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    case 3: return launch_gemm<3, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    case 4: return launch_gemm<4, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    case 5: return launch_gemm<5, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    case 6: return launch_gemm<6, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
-    default: return launch_gemm<7, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 1: return launch_gemm<FMT, 1, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 2: return launch_gemm<FMT, 2, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 3: return launch_gemm<FMT, 3, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 4: return launch_gemm<FMT, 4, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 5: return launch_gemm<FMT, 5, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    case 6: return launch_gemm<FMT, 6, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
+    default: return launch_gemm<FMT, 7, G32, XF32, ADD, SPLIT>(x, wq, ws, y, part, M, N, K, group, p, s);
   }
 }
 
-template <bool G32, bool XF32>
+template <int FMT, bool G32, bool XF32>
 static int gemm_dispatch(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
                          int K, int group, int add, const GemmPlan& p, hipStream_t s) {
   if (p.splits > 1) {
-    int st = gemm_mb<G32, XF32, false, true>(x, wq, ws, y, part, M, N, K, group, p, s);
+    int st = gemm_mb<FMT, G32, XF32, false, true>(x, wq, ws, y, part, M, N, K, group, p, s);
     if (st != AQ_OK) return st;
     const int64_t count = (int64_t)M * N;
     int64_t blocks = (count / 4 + 255) / 256;
@@ -348,19 +403,21 @@ static int gemm_dispatch(const void* x, const uint32_t* wq, const uint16_t* ws, 
     hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, s, part, y, count, p.splits, add);
     return launch_status();
   }
-  return add ? gemm_mb<G32, XF32, true, false>(x, wq, ws, y, part, M, N, K, group, p, s)
-             : gemm_mb<G32, XF32, false, false>(x, wq, ws, y, part, M, N, K, group, p, s);
+  return add ? gemm_mb<FMT, G32, XF32, true, false>(x, wq, ws, y, part, M, N, K, group, p, s)
+             : gemm_mb<FMT, G32, XF32, false, false>(x, wq, ws, y, part, M, N, K, group, p, s);
 }
 
+template <int FMT>
 static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_t* ws, float* y, int64_t m,
                       int64_t n, int64_t k, int32_t group, int32_t add, void* workspace, int64_t ws_bytes,
                       void* stream) {
   if (!x || !wq || !ws || !y) return AQ_ERR_NULL;
-  if (m <= 0 || n <= 0 || k <= 0 || k % 32) return AQ_ERR_SHAPE;
+  if (m <= 0 || n <= 0 || k <= 0 || k % (FMT == kT2 ? 128 : 32)) return AQ_ERR_SHAPE;
   if (m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return AQ_ERR_SHAPE;
-  if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
+  if (FMT == kQ4 && (group <= 0 || group % 8 || k % group)) return AQ_ERR_GROUP;
   // buffer offsets are 32-bit: each operand must stay under 2 GiB
-  if (m * k * (xf32 ? 4 : 2) >= ((int64_t)1 << 31) || n * k / 2 >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
+  if (m * k * (xf32 ? 4 : 2) >= ((int64_t)1 << 31) || n * k / (FMT == kT2 ? 4 : 2) >= ((int64_t)1 << 31))
+    return AQ_ERR_CAPACITY;
   if (!aligned(wq, 16) || !aligned(x, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int M = (int)m, N = (int)n, K = (int)k;
@@ -370,11 +427,12 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
     p.sup_per_split = (K + kSuper - 1) / kSuper;
   }
   float* part = static_cast<float*>(workspace);
-  const bool g32 = group % 32 == 0;
-  if (xf32) return g32 ? gemm_dispatch<true, true>(x, wq, ws, y, part, M, N, K, group, add, p, s)
-                       : gemm_dispatch<false, true>(x, wq, ws, y, part, M, N, K, group, add, p, s);
-  return g32 ? gemm_dispatch<true, false>(x, wq, ws, y, part, M, N, K, group, add, p, s)
-             : gemm_dispatch<false, false>(x, wq, ws, y, part, M, N, K, group, add, p, s);
+  const bool g32 = FMT == kT2 || group % 32 == 0;
+  if (FMT == kT2) group = 128;
+  if (xf32) return g32 ? gemm_dispatch<FMT, true, true>(x, wq, ws, y, part, M, N, K, group, add, p, s)
+                       : gemm_dispatch<FMT, false, true>(x, wq, ws, y, part, M, N, K, group, add, p, s);
+  return g32 ? gemm_dispatch<FMT, true, false>(x, wq, ws, y, part, M, N, K, group, add, p, s)
+             : gemm_dispatch<FMT, false, false>(x, wq, ws, y, part, M, N, K, group, add, p, s);
 }
 
 }  // namespace aq
@@ -382,11 +440,21 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
 extern "C" int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y,
                           int64_t m, int64_t n, int64_t k, int32_t group, int32_t add, void* workspace,
                           int64_t workspace_bytes, void* stream) {
-  return aq::gemm_entry(x, x_is_f32, wq, ws, y, m, n, k, group, add, workspace, workspace_bytes, stream);
+  return aq::gemm_entry<aq::kQ4>(x, x_is_f32, wq, ws, y, m, n, k, group, add, workspace, workspace_bytes, stream);
 }
 
+extern "C" int aq_gemm_t2(const void* x, int32_t x_is_f32, const uint32_t* w, const uint16_t* s, float* y, int64_t m,
+                          int64_t n, int64_t k, int32_t add, void* workspace, int64_t workspace_bytes, void* stream) {
+  return aq::gemm_entry<aq::kT2>(x, x_is_f32, w, s, y, m, n, k, 128, add, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k);
 extern "C" int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return 0;
   const aq::GemmPlan p = aq::plan_gemm((int)m, (int)n, (int)k);
   return aq::gemm_workspace_bytes(p, (int)m, (int)n);
+}
+
+extern "C" int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  return aq_gemm_q4_workspace_bytes(m, n, k);
 }

@@ -1,0 +1,303 @@
+// Ternary (T2W) matrix-vector products and the fp16-pair (X2H) producers, gfx950.
+//
+// Arithmetic: y[n] = sum over 128-groups g of s[g, n] * sum_{k in g} (code(k, n) - 1) * x[k], codes of T2W words
+// (uint32 [K/16, N], code of (n, k) in bits 2*(k%16) of word (k/16)*N + n), x given as fp16 pairs. This is
+// bonsai/kernels/kernels.mojo:189-325 (``_group_dot8`` / ``packed_linear``) and :437-448 (``packed_reduce``); the
+// reference accumulates each group in fp16 chains, this build decodes exactly and accumulates in fp32.
+//
+// Decode (HBM-bound: 0.27 B per weight, so ~1.5 VALU ops per weight is the budget). For code position j <= 4 of a
+// 16-bit half, (word & (0x00030003 << 2j)) | 0x64006400 is the fp16 pair (1024 + c_j * 4^j, 1024 + c_{j+8} * 4^j)
+// exactly (the code lands in mantissa bits 2j, 2j+1); subtracting 1024 + 4^j leaves (c - 1) * 4^j exactly, and
+// v_dot2_f32_f16 against the x pair pre-scaled by 4^-j accumulates (c - 1) * x in fp32 with exact products. Positions
+// 5..7 are the same after one shift by 10. That is 25 VALU ops per 16 weights, no table and no bias to cancel.
+#include "aq_common.h"
+
+namespace aq {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Scale of the x pair used with code position j (0..7) of a 16-bit half.
+__device__ __forceinline__ float t2_xscale(int j) {
+  const int e = j <= 4 ? j : j - 5;
+  return 1.0f / (float)(1 << (2 * e));
+}
+
+// sum_{j<16} (code_j - 1) * x_j for one T2W word; xp[j] = fp16 pair (x[j], x[j+8]) * 4^-e(j).
+__device__ __forceinline__ float t2_word_dot(uint32_t w, const uint32_t* xp, float acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = j <= 4 ? j : j - 5;
+    const uint32_t src = j <= 4 ? w : (w >> 10);
+    const uint32_t bits = (src & (0x00030003u << (2 * e))) | 0x64006400u;
+    half2v h = __builtin_bit_cast(half2v, bits);
+    const _Float16 bias = (_Float16)(1024.0f + (float)(1 << (2 * e)));
+    h = h - half2v{bias, bias};
+    acc = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc, false);
+  }
+  return acc;
+}
+
+// Workgroup (column tile ct, split sp): columns [256 ct, +256) (lane l -> columns 4l..4l+3 of the tile, all four
+// waves), k-rows (16 k each) [sp * krows_wg, +krows_wg) divided among the four waves (whole 128-groups each).
+// MODE 0: fused GEMV, the last workgroup of a column tile to finish sums the split partials in split order.
+// MODE 1: reference partials (packed_linear): each workgroup covers 1024 k and writes partial[sp][n].
+template <int MODE, bool VEC4>
+__global__ __launch_bounds__(256) void k_t2_gemv(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
+                                                 const uint16_t* __restrict__ sc, float* __restrict__ y,
+                                                 float* __restrict__ part, int* __restrict__ counters, int N, int K,
+                                                 int krows_wg, int splits) {
+  extern __shared__ uint32_t xs[];  // [krows_wg][8] scaled x pairs, then [4][256] floats for the wave reduction
+  float* red = reinterpret_cast<float*>(xs + krows_wg * 8);
+  __shared__ int last;
+  const int ct = blockIdx.x / splits;
+  const int sp = blockIdx.x - ct * splits;
+  const int kr0 = sp * krows_wg;
+  const int krows_total = K >> 4;
+  const int nrows = min(krows_wg, krows_total - kr0);
+
+  // x' for this workgroup's k-rows: pair j of row r = (x[16r + j], x[16r + j + 8]) * 4^-e(j)
+  for (int i = threadIdx.x; i < nrows * 8; i += 256) {
+    const int r = i >> 3, j = i & 7;
+    const int k = (kr0 + r) * 16 + j;
+    const uint32_t lo = x2h[k >> 1], hi = x2h[(k + 8) >> 1];
+    const float a = half_bits_to_float((uint16_t)(k & 1 ? lo >> 16 : lo & 0xFFFF));
+    const float b = half_bits_to_float((uint16_t)((k + 8) & 1 ? hi >> 16 : hi & 0xFFFF));
+    const float f = t2_xscale(j);
+    xs[i] = (uint32_t)float_to_half_bits(a * f) | ((uint32_t)float_to_half_bits(b * f) << 16);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = ct * 256 + lane * 4;
+  const int groups = (nrows + 7) >> 3;              // 128-groups in this workgroup
+  const int gpw = (groups + 3) >> 2;                // groups per wave
+  const int g0 = wave * gpw, g1 = min(groups, g0 + gpw);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(w), (short)0,
+                                                                      (int)min((size_t)krows_total * N * 4,
+                                                                               (size_t)0x7FFFFFFF),
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(sc), (short)0,
+                                                                       (int)((size_t)(K >> 7) * N * 2), 0x00020000);
+  float tot[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int g = g0; g < g1; ++g) {
+    const int r0 = g * 8;
+    uint4 wv[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint32_t row = (uint32_t)(kr0 + r0 + r);
+      if constexpr (VEC4) {
+        const uint32_t off = n0 < N ? (row * (uint32_t)N + n0) * 4 : 0x80000000u;
+        wv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+      } else {
+        uint32_t v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t off = n0 + c < N ? (row * (uint32_t)N + n0 + c) * 4 : 0x80000000u;
+          v[c] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
+        }
+        wv[r] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    }
+    float s4[4];
+    const uint32_t grow = (uint32_t)((kr0 + r0) >> 3);  // 128-group index
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t off = n0 + c < N ? (grow * (uint32_t)N + n0 + c) * 2 : 0x80000000u;
+      s4[c] = half_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(srs, off, 0, 0));
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      uint32_t xp[8];
+      *reinterpret_cast<uint4*>(xp) = *reinterpret_cast<const uint4*>(xs + (r0 + r) * 8);
+      *reinterpret_cast<uint4*>(xp + 4) = *reinterpret_cast<const uint4*>(xs + (r0 + r) * 8 + 4);
+      acc[0] = t2_word_dot(wv[r].x, xp, acc[0]);
+      acc[1] = t2_word_dot(wv[r].y, xp, acc[1]);
+      acc[2] = t2_word_dot(wv[r].z, xp, acc[2]);
+      acc[3] = t2_word_dot(wv[r].w, xp, acc[3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tot[c] = fmaf(acc[c], s4[c], tot[c]);
+  }
+
+  // waves -> one partial per column (wave order)
+  *reinterpret_cast<float4*>(red + (wave * 256 + lane * 4)) = make_float4(tot[0], tot[1], tot[2], tot[3]);
+  __syncthreads();
+  const int n = ct * 256 + threadIdx.x;
+  float v = ((red[threadIdx.x] + red[256 + threadIdx.x]) + red[512 + threadIdx.x]) + red[768 + threadIdx.x];
+  if (MODE == 1 || splits == 1) {
+    if (n < N) {
+      if (MODE == 1) part[(size_t)sp * N + n] = v;
+      else y[n] = v;
+    }
+    return;
+  }
+  if (n < N) part[(size_t)sp * N + n] = v;
+  __threadfence();  // release: this workgroup's partials before its arrival is counted
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicAdd(&counters[ct], 1) == splits - 1;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // acquire: every other split's partials are visible
+  if (n < N) {
+    float acc = 0.f;
+    for (int s2 = 0; s2 < splits; ++s2) acc += __builtin_nontemporal_load(part + (size_t)s2 * N + n);
+    y[n] = acc;
+  }
+  if (threadIdx.x == 0) counters[ct] = 0;  // ready for the next call
+}
+
+// y[n] = sum_g partials[g][n] in g order (bonsai/kernels/kernels.mojo:437-448, packed_reduce).
+__global__ __launch_bounds__(256) void k_t2_reduce(const float* __restrict__ part, float* __restrict__ y, int N,
+                                                   int groups) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  float acc = 0.f;
+  for (int g = 0; g < groups; ++g) acc += part[(size_t)g * N + n];
+  y[n] = acc;
+}
+
+// ---- X2H producers (qwen3/kernels/qwen3k.mojo:17-59) ----
+
+__global__ void k_pack_half(const float* __restrict__ x, uint32_t* __restrict__ q, int64_t pairs) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < pairs; i += (int64_t)gridDim.x * 256)
+    q[i] = (uint32_t)float_to_half_bits(x[2 * i]) | ((uint32_t)float_to_half_bits(x[2 * i + 1]) << 16);
+}
+
+// One workgroup per row: q[row] = pack(x[row] / rms(x[row]) * w), eps as given.
+__global__ __launch_bounds__(256) void k_rmsnorm_pack(const float* __restrict__ x, const float* __restrict__ w,
+                                                      uint32_t* __restrict__ q, int n, float eps) {
+  __shared__ float red[4];
+  const float* xr = x + (size_t)blockIdx.x * n;
+  uint32_t* qr = q + (size_t)blockIdx.x * (n / 2);
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)n + eps);
+  for (int i = threadIdx.x; i < n / 2; i += 256)
+    qr[i] = (uint32_t)float_to_half_bits(xr[2 * i] * r * w[2 * i]) |
+            ((uint32_t)float_to_half_bits(xr[2 * i + 1] * r * w[2 * i + 1]) << 16);
+}
+
+// q[row] = pack(silu(gate) * up), rows of gu = gate (n) | up (n).
+__global__ void k_swiglu_pack(const float* __restrict__ gu, uint32_t* __restrict__ q, int n, int rows) {
+  const int64_t pairs = (int64_t)rows * (n / 2);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < pairs; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / (n / 2);
+    const int c = (int)(i - row * (n / 2)) * 2;
+    const float* g = gu + row * 2 * n;
+    const float a = silu(g[c]) * g[n + c];
+    const float b = silu(g[c + 1]) * g[n + c + 1];
+    q[i] = (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+  }
+}
+
+static int t2_check(const void* x2h, const void* w, const void* s, int64_t n, int64_t k) {
+  if (!x2h || !w || !s) return AQ_ERR_NULL;
+  if (n <= 0 || k <= 0 || k % 128) return AQ_ERR_SHAPE;
+  if (n > (1 << 26) || k > (1 << 24) || (k / 16) * n * 4 >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
+  if (!aligned(w, 16)) return AQ_ERR_ALIGN;
+  return AQ_OK;
+}
+
+template <int MODE>
+static int launch_t2(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, float* part, int* counters,
+                     int N, int K, int krows_wg, int splits, hipStream_t st) {
+  const int ctiles = (N + 255) / 256;
+  const size_t lds = (size_t)krows_wg * 8 * 4 + 4 * 256 * 4;
+  const bool vec4 = (N % 4) == 0;
+  if (vec4)
+    hipLaunchKernelGGL((k_t2_gemv<MODE, true>), dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, y, part,
+                       counters, N, K, krows_wg, splits);
+  else
+    hipLaunchKernelGGL((k_t2_gemv<MODE, false>), dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, y, part,
+                       counters, N, K, krows_wg, splits);
+  return launch_status();
+}
+
+}  // namespace aq
+
+using namespace aq;
+
+// Workspace layout, fixed for every shape so that counters never land on an earlier call's partials:
+// [0, 64 KiB) arrival counters (one int per 256-column tile, all zero between calls), then the fp32 partials.
+constexpr int64_t kT2CounterBytes = 64 * 1024;
+
+extern "C" int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k) {
+  if (n <= 0 || k <= 0) return 0;
+  const int64_t splits = (k + 511) / 512;
+  return splits > 1 ? kT2CounterBytes + splits * n * 4 : 0;
+}
+
+extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int64_t n, int64_t k,
+                          void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = t2_check(x2h, w, s, n, k);
+  if (st) return st;
+  if (!y) return AQ_ERR_NULL;
+  const int N = (int)n, K = (int)k;
+  int splits = (K + 511) / 512;
+  int krows_wg = 32;  // 512 k: one 128-group per wave
+  float* part = nullptr;
+  int* counters = nullptr;
+  if (splits > 1) {
+    const int64_t need = aq_t2_gemv_workspace_bytes(n, k);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 16) || (n + 255) / 256 > kT2CounterBytes / 4) {
+      splits = 1;  // no workspace: one workgroup per column tile covers all of K
+      krows_wg = K / 16;
+    } else {
+      counters = static_cast<int*>(workspace);
+      part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kT2CounterBytes);
+    }
+  }
+  return launch_t2<0>(x2h, w, s, y, part, counters, N, K, krows_wg, splits, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials,
+                                   int64_t n, int64_t k, void* stream) {
+  int st = t2_check(x2h, w, s, n, k);
+  if (st) return st;
+  if (!partials) return AQ_ERR_NULL;
+  const int splits = (int)((k + 1023) / 1024);
+  return launch_t2<1>(x2h, w, s, nullptr, partials, nullptr, (int)n, (int)k, 64, splits,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int aq_t2_packed_reduce(const float* partials, float* y, int64_t n, int32_t groups, void* stream) {
+  if (!partials || !y) return AQ_ERR_NULL;
+  if (n <= 0 || groups <= 0 || n > (1 << 30)) return AQ_ERR_SHAPE;
+  hipLaunchKernelGGL(k_t2_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), partials, y, (int)n, groups);
+  return launch_status();
+}
+
+extern "C" int aq_pack_half(const float* x, uint32_t* q, int64_t count, void* stream) {
+  if (!x || !q) return AQ_ERR_NULL;
+  if (count <= 0 || count % 2) return AQ_ERR_SHAPE;
+  int64_t blocks = (count / 2 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_pack_half, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), x, q,
+                     count / 2);
+  return launch_status();
+}
+
+extern "C" int aq_rmsnorm_pack(const float* x, const float* w, uint32_t* q, int64_t rows, int64_t n, float eps,
+                               void* stream) {
+  if (!x || !w || !q) return AQ_ERR_NULL;
+  if (rows <= 0 || n <= 0 || n % 2 || rows > (1 << 30)) return AQ_ERR_SHAPE;
+  hipLaunchKernelGGL(k_rmsnorm_pack, dim3((unsigned)rows), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), x, w,
+                     q, (int)n, eps);
+  return launch_status();
+}
+
+extern "C" int aq_swiglu_pack(const float* gu, uint32_t* q, int64_t rows, int64_t n, void* stream) {
+  if (!gu || !q) return AQ_ERR_NULL;
+  if (rows <= 0 || n <= 0 || n % 2) return AQ_ERR_SHAPE;
+  int64_t blocks = (rows * n / 2 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_swiglu_pack, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), gu,
+                     q, (int)n, (int)rows);
+  return launch_status();
+}

@@ -1,0 +1,161 @@
+"""Ternary (T2W) GEMV and the X2H producers on the GPU vs the oracle: packed_linear / packed_reduce / pack_half /
+rmsnorm_pack / swiglu_pack."""
+import numpy as np
+import pytest
+
+from _util import rel_inf, to_dev, to_np
+from oracle import aq_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _ops():
+    from aq import ops
+    return ops
+
+
+def _kat(rng, n, k):
+    """Integer-exact ternary inputs: codes uniform in {0,1,2}, power-of-two scales, small-integer x."""
+    codes = rng.integers(0, 3, size=(n, k))
+    s = np.exp2(rng.integers(-3, 2, size=(k // 128, n))).astype(np.float16)
+    x = rng.integers(-3, 4, size=k).astype(np.float32)
+    return codes, s, x
+
+
+def _exact(codes, s, x):
+    n, k = codes.shape
+    s8 = (s.astype(np.float64) * 8).astype(np.int64)                 # [K/128, N] integers
+    w8 = (codes.astype(np.int64) - 1) * np.repeat(s8.T, 128, axis=1)  # [N, K]
+    return (w8 @ x.astype(np.int64)).astype(np.float64) / 8.0
+
+
+@pytest.mark.parametrize("n,k", [(256, 512), (12288, 4096), (4096, 12288), (300, 1024), (6, 128), (1000, 2176),
+                                 (37, 640)])
+def test_t2_gemv_kat_bit_exact(dev, n, k):
+    import torch
+    rng = np.random.default_rng(n + k)
+    codes, s, x = _kat(rng, n, k)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    _ops().t2_gemv(to_dev(orc.x2h_pack(x), dev), to_dev(orc.t2w_pack(codes), dev), to_dev(s, dev), y)
+    np.testing.assert_array_equal(to_np(y), _exact(codes, s, x).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["gate", "down"])
+def test_c2_gemv_parity(dev, name):
+    """C2: Qwen3-8B gate (12288 x 4096) and down (4096 x 12288), fp16 x."""
+    import torch
+    from aq import synth
+    rng = np.random.default_rng(2)
+    n, k = {"gate": (12288, 4096), "down": (4096, 12288)}[name]
+    w, s = synth.ternary_matrix(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    xh = orc.x2h_pack(x)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    _ops().t2_gemv(to_dev(xh, dev), to_dev(w, dev), to_dev(s, dev), y)
+    assert rel_inf(to_np(y), orc.ternary_gemv(w, s, xh, n, k)) < TOL
+
+
+def test_t2_gemv_without_workspace(dev):
+    import torch
+    rng = np.random.default_rng(5)
+    n, k = 1024, 4096
+    codes, s, x = _kat(rng, n, k)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    torch.ops.aq.t2_gemv(to_dev(orc.x2h_pack(x), dev), to_dev(orc.t2w_pack(codes), dev), to_dev(s, dev), y,
+                         torch.empty(8, dtype=torch.uint8, device=dev))
+    np.testing.assert_array_equal(to_np(y), _exact(codes, s, x).astype(np.float32))
+
+
+@pytest.mark.parametrize("n,k", [(640, 4096), (100, 2176)])
+def test_packed_linear_and_reduce(dev, n, k):
+    """The reference's two-kernel interface: partials [ceil(K/1024), N], then their sum."""
+    import torch
+    rng = np.random.default_rng(9)
+    w, s = __import__("aq").synth.ternary_matrix(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    xh = orc.x2h_pack(x)
+    g = (k + 1023) // 1024
+    part = torch.empty((g, n), dtype=torch.float32, device=dev)
+    _ops().t2_packed_linear(to_dev(xh, dev), to_dev(w, dev), to_dev(s, dev), part)
+    ref = orc.ternary_partials(w, s, xh, n, k)
+    assert rel_inf(to_np(part), ref) < TOL
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    _ops().t2_packed_reduce(part, y)
+    np.testing.assert_allclose(to_np(y), to_np(part).astype(np.float64).sum(0), rtol=1e-6, atol=1e-6)
+
+
+def test_pack_half_bit_exact(dev):
+    import torch
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(4094).astype(np.float32),
+                        np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11], np.float32)])  # ties to even
+    q = torch.empty(2048, dtype=torch.int32, device=dev)
+    _ops().pack_half(to_dev(x, dev), q)
+    np.testing.assert_array_equal(to_np(q).view(np.uint32), orc.x2h_pack(x))
+
+
+def test_rmsnorm_and_swiglu_pack(dev):
+    import torch
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((3, 4096)).astype(np.float32)
+    w = rng.standard_normal(4096).astype(np.float32)
+    q = torch.empty((3, 2048), dtype=torch.int32, device=dev)
+    _ops().rmsnorm_pack(to_dev(x, dev), to_dev(w, dev), q)
+    got = orc.x2h_unpack(to_np(q).view(np.uint32))
+    ref = np.stack([orc.x2h_unpack(orc.rmsnorm_pack(x[i], w)) for i in range(3)])
+    np.testing.assert_allclose(got, ref, rtol=2 ** -10, atol=1e-6)
+    gu = rng.standard_normal((2, 2 * 1024)).astype(np.float32)
+    q = torch.empty((2, 512), dtype=torch.int32, device=dev)
+    _ops().swiglu_pack(to_dev(gu, dev), q)
+    got = orc.x2h_unpack(to_np(q).view(np.uint32))
+    ref = np.stack([orc.x2h_unpack(orc.swiglu_pack(gu[i], 1024)) for i in range(2)])
+    np.testing.assert_allclose(got, ref, rtol=2 ** -10, atol=1e-6)
+
+
+def _gemm_t2(x, w, s, dev, add_to=None):
+    import torch
+    m, n = x.shape[0], w.shape[1]
+    y = torch.zeros((m, n), dtype=torch.float32, device=dev) if add_to is None else to_dev(add_to, dev)
+    _ops().gemm_t2(to_dev(x, dev), to_dev(w, dev), to_dev(s, dev), y, add=add_to is not None)
+    return to_np(y)
+
+
+@pytest.mark.parametrize("m,n,k,xf32", [(16, 64, 128, False), (412, 256, 1024, False), (100, 300, 256, True),
+                                        (412, 12288, 4096, False), (412, 4096, 12288, False), (1, 16, 128, False),
+                                        (33, 100, 640, True)])
+def test_gemm_t2_kat_bit_exact(dev, m, n, k, xf32):
+    """Integer-valued X and power-of-two scales: exact in fp16 MFMA with fp32 accumulation."""
+    rng = np.random.default_rng(m + n + k)
+    codes = rng.integers(0, 3, size=(n, k))
+    s = np.exp2(rng.integers(-3, 2, size=(k // 128, n))).astype(np.float16)
+    x = rng.integers(-3, 4, size=(m, k)).astype(np.float32 if xf32 else np.float16)
+    got = _gemm_t2(x, orc.t2w_pack(codes), s, dev)
+    s8 = (s.astype(np.float64) * 8).astype(np.int64)
+    w8 = (codes.astype(np.int64) - 1) * np.repeat(s8.T, 128, axis=1)
+    exact = (x.astype(np.int64) @ w8.T).astype(np.float64) / 8.0
+    np.testing.assert_array_equal(got, exact.astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["gate", "down"])
+def test_c2_gemm_parity(dev, name):
+    """C2 GEMM at M = 412, fp16 activations."""
+    from aq import synth
+    rng = np.random.default_rng(22)
+    n, k = {"gate": (12288, 4096), "down": (4096, 12288)}[name]
+    w, s = synth.ternary_matrix(rng, n, k)
+    x = rng.standard_normal((412, k)).astype(np.float16)
+    got = _gemm_t2(x, w, s, dev)
+    assert rel_inf(got, orc.ternary_gemm(x.astype(np.float32), w, s)) < 1e-2
+
+
+def test_gemm_t2_add(dev):
+    rng = np.random.default_rng(23)
+    n, k, m = 512, 1024, 64
+    from aq import synth
+    w, s = synth.ternary_matrix(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = _gemm_t2(x, w, s, dev, add_to=y0)
+    assert rel_inf(got, orc.ternary_gemm(x, w, s) + y0) < 1e-2
