@@ -79,6 +79,69 @@ int aq_gemm_t2(const void* x, int32_t x_is_f32, const uint32_t* w, const uint16_
                int64_t k, int32_t add, void* workspace, int64_t workspace_bytes, void* stream);
 int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
+/* ---- mixture of experts ----------------------------------------------------------------------------------------------
+ * Grouped int4 GEMM over experts. Work tile it < ntiles[0] (device) is (tiles[2it] = expert e, tiles[2it+1] = first
+ * grouped row g0); its tm rows g0 .. g0+tm-1 read X row src[g] (a token of x [x_rows, K]; -1 = padding row, zeros)
+ * or row g itself when src is NULL. W holds the experts stacked: expert e's n rows start at row e*n (Q4W
+ * [experts*n, K/8], fp16 scales [experts*n, K/group]).
+ *   swiglu = 0: out fp32 [rows_total, n], out[g] = X_g . W_e^T.
+ *   swiglu = 1: W_e rows are gate (n/2) | up (n/2); out fp16 [rows_total, n/2], out[g, j] = silu(g_j) * u_j.
+ * max_tiles bounds the grid (aq_moe_group_max_tiles); tm a multiple of 16 up to 112. x fp16 (x_is_f32 = 0) or fp32.
+ * Replaces: p_gemm_q4g (lfm2moe/kernels/mk.mojo:208-257) with p_gather (:164-176) and p_silu_mul (:179-186) folded in,
+ * and t_moe_gate_up / t_moe_down (qwen3moe/kernels/moek.mojo:560-608). */
+int aq_moe_gemm_q4(const void* x, int32_t x_is_f32, int64_t x_rows, const int32_t* src, const uint32_t* wq,
+                   const uint16_t* ws, int64_t experts, int64_t n, int64_t k, int32_t group, const int32_t* tiles,
+                   const int32_t* ntiles, int32_t max_tiles, int32_t tm, int64_t rows_total, int32_t swiglu, void* out,
+                   void* stream);
+
+/* Top-k routing: per token, the k largest of `experts` logits (descending; the lowest index among equals) and their
+ * weights exp(l_k - l_max) / sum_top exp(l_j - l_max) (softmax, top-k, renormalise). experts <= 256, topk <= 8.
+ * Replaces: route / p_route (qwen3moe/kernels/moek.mojo:156-197,385-425). */
+int aq_moe_route(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts, int32_t topk,
+                 void* stream);
+
+/* Grouping of the routed entries i = t*topk + k by expert (one workgroup, deterministic): counts[e]; offs[e] =
+ * exclusive prefix sum of the counts padded to multiples of tm (offs[experts] = rows used); slot[i] = grouped row
+ * (ascending i within an expert); src[row] = token (-1 on padding and unused rows < max_rows); work tiles (e, row)
+ * every tm rows of each expert, in expert order, and their number ntiles[0]. max_rows >= aq_moe_group_max_rows,
+ * max_tiles >= aq_moe_group_max_tiles. Replaces: p_group (lfm2moe/kernels/mk.mojo:123-161). */
+int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm, int32_t* counts,
+                 int32_t* offs, int32_t* slot, int32_t* src, int64_t max_rows, int32_t* tiles, int32_t max_tiles,
+                 int32_t* ntiles, void* stream);
+int64_t aq_moe_group_max_rows(int64_t tokens, int32_t topk, int32_t experts, int32_t tm);
+int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t experts, int32_t tm);
+
+/* Per-expert lists of entries: lists[e*cap + r] = the r-th entry i (ascending) with ids[i] == e, counts[e]; with
+ * items != NULL also the work items (e, c) for c = 0, items_tt, ... < counts[e] in expert order and nitems[0].
+ * scratch: >= (experts + 1) + 4 * tokens * topk + 1 ints of device memory. Replaces: p_expert_lists and
+ * p_expert_items (qwen3moe/kernels/moek.mojo:432-442,548-557; cap = PMAX there). */
+int aq_moe_expert_lists(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t cap,
+                        int32_t* lists, int32_t* counts, int32_t items_tt, int32_t* items, int32_t max_items,
+                        int32_t* nitems, int32_t* scratch, int64_t scratch_ints, void* stream);
+
+/* y[t, c] = (add ? y[t, c] : 0) + sum_{k < topk} weights[t, k] * yd[slot[t*topk + k], c], k in order; slot NULL means
+ * row t*topk + k. Replaces: p_combine (lfm2moe/kernels/mk.mojo:189-199) and, with slot NULL and add = 1, p_moe_sum
+ * (qwen3moe/kernels/moek.mojo:479-488). d % 4 == 0; a slot outside [0, yd_rows) contributes nothing. */
+int aq_moe_combine(const float* yd, int64_t yd_rows, const int32_t* slot, const float* weights, float* y,
+                   int64_t tokens, int64_t d, int32_t topk, int32_t add, void* stream);
+
+/* Decode (one token): a[e, j] = silu(W[ids[e]*2f + j] . x) * (W[ids[e]*2f + f + j] . x), e < topk, j < f.
+ * An id outside [0, experts) gives a[e] = 0 (the reference does not check).
+ * Replaces: moe_gate_up (qwen3moe/kernels/moek.mojo:200-210; lfm2moe/kernels/mk.mojo:94-104). */
+int aq_moe_gate_up_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids, const float* x,
+                      float* a, int64_t f, int64_t k, int32_t group, int32_t topk, void* stream);
+
+/* Decode: y[r] = (add ? y[r] : 0) + sum_e weights[e] * W[ids[e]*d + r] . a[e], e in order.
+ * An id outside [0, experts) contributes nothing.
+ * Replaces: moe_down (qwen3moe/kernels/moek.mojo:213-223, add = 1; lfm2moe/kernels/mk.mojo:107-118, add = 0). */
+int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids, const float* weights,
+                   const float* a, float* y, int64_t d, int64_t f, int32_t group, int32_t topk, int32_t add,
+                   void* stream);
+
+/* Router: y[t, r] = W[r] . x[t], fp32 W [n, k]. Replaces: gemv_f32 / p_gemv_f32 (qwen3moe/kernels/moek.mojo:143-153,
+ * 284-295). */
+int aq_gemv_f32(const float* w, const float* x, float* y, int64_t n, int64_t k, int32_t tokens, void* stream);
+
 /* ---- ternary (T2W) matrix-vector products, decode ---------------------------------------------------------------
  * y[n] = sum_k (code(k, n) - 1) * s[k/128, n] * x[k], x as X2H fp16 pairs [K/2], T2W w [K/16, N], s fp16 [K/128, N],
  * fp32 accumulation (the reference accumulates groups in fp16). Requires K % 128 == 0, 16-byte aligned w.

@@ -25,6 +25,16 @@ SIGNATURES: dict[str, list] = {
     "aq_gemm_q4_workspace_bytes": [_i64, _i64, _i64],
     "aq_gemm_t2": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "aq_gemm_t2_workspace_bytes": [_i64, _i64, _i64],
+    "aq_moe_gemm_q4": [_p, _i32, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _i32, _i32, _i64, _i32, _p, _p],
+    "aq_moe_route": [_p, _p, _p, _i64, _i32, _i32, _p],
+    "aq_moe_group": [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
+    "aq_moe_group_max_rows": [_i64, _i32, _i32, _i32],
+    "aq_moe_group_max_tiles": [_i64, _i32, _i32, _i32],
+    "aq_moe_expert_lists": [_p, _i64, _i32, _i32, _i32, _p, _p, _i32, _p, _i32, _p, _p, _i64, _p],
+    "aq_moe_combine": [_p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
+    "aq_moe_gate_up_q4": [_p, _p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
+    "aq_moe_down_q4": [_p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p],
+    "aq_gemv_f32": [_p, _p, _p, _i64, _i64, _i32, _p],
     "aq_t2_gemv": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p],
     "aq_t2_gemv_workspace_bytes": [_i64, _i64],
     "aq_t2_packed_linear": [_p, _p, _p, _p, _i64, _i64, _p],
@@ -34,7 +44,8 @@ SIGNATURES: dict[str, list] = {
     "aq_swiglu_pack": [_p, _p, _i64, _i64, _p],
 }
 RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64, "aq_t2_gemv_workspace_bytes": ctypes.c_int64,
-            "aq_gemm_t2_workspace_bytes": ctypes.c_int64}
+            "aq_gemm_t2_workspace_bytes": ctypes.c_int64, "aq_moe_group_max_rows": ctypes.c_int64,
+            "aq_moe_group_max_tiles": ctypes.c_int32}
 
 _lib = None
 

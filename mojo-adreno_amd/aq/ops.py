@@ -271,3 +271,125 @@ def gemm_t2(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, y: torch.Tensor, 
     """``Y (+)= X . deq_T2(W)^T`` on MFMA: X fp16/fp32 [M, K], T2W ``w [K/16, N]``, fp16 ``s [K/128, N]``, Y fp32."""
     need = _lib.lib().aq_gemm_t2_workspace_bytes(x.shape[0], w.shape[1], w.shape[0] * 16)
     torch.ops.aq.gemm_t2(x, w, s, y, add, workspace(x.device, need))
+
+
+# ---- mixture of experts -------------------------------------------------------------------------------------------
+
+_LIB.define("moe_route(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk) -> ()")
+_LIB.define("moe_group(Tensor ids, int experts, int tm, Tensor(a!) counts, Tensor(b!) offs, Tensor(c!) slot, "
+            "Tensor(d!) src, Tensor(e!) tiles, Tensor(f!) ntiles) -> ()")
+_LIB.define("moe_gemm_q4(Tensor x, Tensor src, Tensor wq, Tensor ws, int experts, int group, Tensor tiles, "
+            "Tensor ntiles, int tm, bool swiglu, Tensor(a!) out) -> ()")
+_LIB.define("moe_combine(Tensor yd, Tensor slot, Tensor weights, Tensor(a!) y, bool add) -> ()")
+_LIB.define("moe_gate_up_q4(Tensor wq, Tensor ws, int experts, Tensor ids, Tensor x, Tensor(a!) a, int group) -> ()")
+_LIB.define("moe_down_q4(Tensor wq, Tensor ws, int experts, Tensor ids, Tensor weights, Tensor a, Tensor(a!) y, "
+            "int group, bool add) -> ()")
+_LIB.define("gemv_f32(Tensor w, Tensor x, Tensor(a!) y) -> ()")
+_LIB.define("moe_expert_lists(Tensor ids, int experts, Tensor(a!) lists, Tensor(b!) counts, int items_tt, "
+            "Tensor(c!) items, Tensor(d!) nitems, Tensor(e!) scratch) -> ()")
+
+
+def _i32(*ts):
+    for t in ts:
+        _check(t.dtype == torch.int32, "index tensors must be int32")
+
+
+def _moe_route_impl(logits, ids, weights, topk):
+    _dev(logits, ids, weights)
+    _i32(ids)
+    _check(logits.dtype == torch.float32 and weights.dtype == torch.float32, "logits/weights must be float32")
+    t, e = logits.shape
+    _check(ids.numel() == t * topk and weights.numel() == t * topk, "ids/weights must be [T, topk]")
+    _lib.call("aq_moe_route", _ptr(logits), _ptr(ids), _ptr(weights), t, e, topk, _stream(logits))
+
+
+def _moe_group_impl(ids, experts, tm, counts, offs, slot, src, tiles, ntiles):
+    _dev(ids, counts, offs, slot, src, tiles, ntiles)
+    _i32(ids, counts, offs, slot, src, tiles, ntiles)
+    t, k = ids.shape
+    _check(counts.numel() == experts and offs.numel() == experts + 1 and slot.numel() == t * k, "bad output sizes")
+    _lib.call("aq_moe_group", _ptr(ids), t, k, experts, tm, _ptr(counts), _ptr(offs), _ptr(slot), _ptr(src),
+              src.numel(), _ptr(tiles), tiles.numel() // 2, _ptr(ntiles), _stream(ids))
+
+
+def _moe_gemm_q4_impl(x, src, wq, ws, experts, group, tiles, ntiles, tm, swiglu, out):
+    _dev(x, wq, ws, tiles, ntiles, out)
+    _u32(wq, "wq")
+    _f16bits(ws, "ws")
+    _i32(tiles, ntiles)
+    _check(x.dtype in (torch.float16, torch.float32), "x must be float16 or float32")
+    rows, kw = wq.shape
+    k = kw * 8
+    _check(rows % experts == 0, "wq rows must be experts * n")
+    n = rows // experts
+    _check(x.dim() == 2 and x.shape[1] == k, "x must be [rows, K]")
+    if swiglu:
+        _check(out.dtype == torch.float16 and out.shape[1] == n // 2, "swiglu out must be float16 [rows_total, n/2]")
+    else:
+        _check(out.dtype == torch.float32 and out.shape[1] == n, "out must be float32 [rows_total, n]")
+    src_ptr = 0
+    if src.numel():
+        _dev(src)
+        _i32(src)
+        src_ptr = _ptr(src)
+    _lib.call("aq_moe_gemm_q4", _ptr(x), int(x.dtype == torch.float32), x.shape[0], src_ptr, _ptr(wq), _ptr(ws),
+              experts, n, k, group, _ptr(tiles), _ptr(ntiles), tiles.numel() // 2, tm, out.shape[0], int(swiglu),
+              _ptr(out), _stream(x))
+
+
+def _moe_combine_impl(yd, slot, weights, y, add):
+    _dev(yd, weights, y)
+    _check(yd.dtype == torch.float32 and y.dtype == torch.float32 and weights.dtype == torch.float32, "float32")
+    t, k = weights.shape
+    d = y.shape[-1]
+    slot_ptr = 0
+    if slot.numel():
+        _dev(slot)
+        _i32(slot)
+        slot_ptr = _ptr(slot)
+    _lib.call("aq_moe_combine", _ptr(yd), yd.shape[0], slot_ptr, _ptr(weights), _ptr(y), t, d, k, int(add),
+              _stream(y))
+
+
+def _moe_gate_up_q4_impl(wq, ws, experts, ids, x, a, group):
+    _dev(wq, ws, ids, x, a)
+    _i32(ids)
+    rows, kw = wq.shape
+    f = rows // experts // 2
+    _lib.call("aq_moe_gate_up_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(x), _ptr(a), f, kw * 8, group,
+              ids.numel(), _stream(x))
+
+
+def _moe_down_q4_impl(wq, ws, experts, ids, weights, a, y, group, add):
+    _dev(wq, ws, ids, weights, a, y)
+    _i32(ids)
+    rows, kw = wq.shape
+    _lib.call("aq_moe_down_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(weights), _ptr(a), _ptr(y),
+              rows // experts, kw * 8, group, ids.numel(), int(add), _stream(y))
+
+
+def _gemv_f32_impl(w, x, y):
+    _dev(w, x, y)
+    n, k = w.shape
+    tokens = x.numel() // k
+    _check(y.numel() == n * tokens, "y must be [tokens, N]")
+    _lib.call("aq_gemv_f32", _ptr(w), _ptr(x), _ptr(y), n, k, tokens, _stream(y))
+
+
+def _moe_expert_lists_impl(ids, experts, lists, counts, items_tt, items, nitems, scratch):
+    _dev(ids, lists, counts, scratch)
+    _i32(ids, lists, counts, scratch)
+    t, k = ids.shape
+    items_ptr = nitems_ptr = 0
+    if items.numel():
+        _dev(items, nitems)
+        items_ptr, nitems_ptr = _ptr(items), _ptr(nitems)
+    _lib.call("aq_moe_expert_lists", _ptr(ids), t, k, experts, lists.shape[1], _ptr(lists), _ptr(counts), items_tt,
+              items_ptr, items.numel() // 2, nitems_ptr, _ptr(scratch), scratch.numel(), _stream(ids))
+
+
+for _name, _fn in (("moe_route", _moe_route_impl), ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl),
+                   ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
+                   ("moe_down_q4", _moe_down_q4_impl), ("gemv_f32", _gemv_f32_impl),
+                   ("moe_expert_lists", _moe_expert_lists_impl)):
+    _LIB.impl(_name, _fn, "CUDA")

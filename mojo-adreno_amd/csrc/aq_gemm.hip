@@ -86,11 +86,34 @@ enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transpose
 // step s takes word s/2, code positions j = 4(s%2) + t and j + 8 (t = 0..3) as fp16 pairs (1024 + c, via mask and
 // OR), minus 1025, times the column's fp16 scale for this 128-group. X is staged with the same pairing: 8-k chunks
 // A (k 0..7 of a 16-k word) and B (k 8..15) interleave as (A[4h+t], B[4h+t]).
-template <int FMT, int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT>
-__global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, const uint32_t* __restrict__ wq,
-                                                 const uint16_t* __restrict__ ws, float* __restrict__ y,
-                                                 float* __restrict__ part, int M, int N, int K, int group,
-                                                 int mtiles, int ntiles, int splits, int sup_per_split) {
+// Kernel arguments (by value). Dense: X [M, K] -> y [M, N]. Grouped (MoE): work tile `it` of tiles[] is (expert e,
+// first grouped row m0); X row of grouped row g is src[g] (a token; -1 = padding, zeros) or g itself when src is
+// null; W rows of expert e start at e * n_per_expert; output rows are grouped rows (rows_total of them).
+struct GemmArgs {
+  const void* x;
+  const uint32_t* w;
+  const uint16_t* s;
+  float* y;
+  float* part;
+  uint16_t* act;           // SwiGLU epilogue output (fp16 bits) [rows_total, F]
+  const int* tiles;        // grouped: (expert, first row) pairs
+  const int* ntiles_dev;   // grouped: number of valid tiles (device)
+  const int* src;          // grouped: token of each grouped row, or null
+  int M, N, K, group, mtiles, ntiles, splits, sup_per_split;
+  int n_per_expert, F, rows_total;
+};
+
+enum { kDense = 0, kGrouped = 1, kGroupedSwiglu = 2 };
+
+template <int FMT, int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT, int MODE>
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
+  const void* __restrict__ xv = ga.x;
+  const uint32_t* __restrict__ wq = ga.w;
+  const uint16_t* __restrict__ ws = ga.s;
+  float* __restrict__ y = ga.y;
+  float* __restrict__ part = ga.part;
+  const int M = ga.M, N = ga.N, K = ga.K, group = ga.group, mtiles = ga.mtiles, ntiles = ga.ntiles;
+  const int splits = ga.splits, sup_per_split = ga.sup_per_split;
   constexpr int BM = 16 * MB;
   constexpr int NW = 16 * NB;                      // columns per wave
   constexpr int UPR = FMT == kT2 ? 8 : 16;          // staging units per row per super-step (16 or 8 k each)
@@ -103,34 +126,52 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, co
   // works through a contiguous run; within a run the m-tiles of one (n-tile, split) are adjacent (they share W).
   int id = blockIdx.x;
   const int nblk = gridDim.x;
-  if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
-  const int mt = id % mtiles;
-  const int rest = id / mtiles;
-  const int sp = rest % splits;
-  const int nt = rest / splits;
-  if (nt >= ntiles) return;
+  int sp = 0, nt, m0, expert = 0;
+  if constexpr (MODE == kDense) {
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int mt = id % mtiles;
+    const int rest = id / mtiles;
+    sp = rest % splits;
+    nt = rest / splits;
+    if (nt >= ntiles) return;
+    m0 = mt * BM;
+  } else {
+    nt = id % ntiles;
+    const int it = id / ntiles;
+    if (it >= *ga.ntiles_dev) return;
+    expert = ga.tiles[2 * it];
+    m0 = ga.tiles[2 * it + 1];
+  }
   const int nsup = (K + kSuper - 1) / kSuper;
   const int ks0 = sp * sup_per_split;
   const int ks1 = min(nsup, ks0 + sup_per_split);
-  const int m0 = mt * BM;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nw0 = nt * (4 * NW) + wave * NW;  // this wave's first column
+  // this wave's first column; SwiGLU: gate columns j0 .. j0 + NW/2 - 1 and up columns F + j0 ..
+  const int nw0 = MODE == kGroupedSwiglu ? nt * (2 * NW) + wave * (NW / 2) : nt * (4 * NW) + wave * NW;
   const int kw = K >> 3;                       // Q4W words per row
   const int gpr = K / group;
 
   const __amdgpu_buffer_rsrc_t xr_rsrc = make_rsrc(xv, (uint32_t)((size_t)M * K * (XF32 ? 4 : 2)));
+  const size_t wrows = MODE == kDense ? (size_t)N : (size_t)ga.n_per_expert * (size_t)ga.mtiles;  // mtiles = experts
   const __amdgpu_buffer_rsrc_t w_rsrc =
-      make_rsrc(wq, (uint32_t)(FMT == kT2 ? (size_t)(K >> 4) * N * 4 : (size_t)N * kw * 4));
+      make_rsrc(wq, (uint32_t)(FMT == kT2 ? (size_t)(K >> 4) * N * 4 : wrows * kw * 4));
   const __amdgpu_buffer_rsrc_t s_rsrc =
-      make_rsrc(ws, (uint32_t)(FMT == kT2 ? (size_t)(K >> 7) * N * 2 : (size_t)N * gpr * 2));
+      make_rsrc(ws, (uint32_t)(FMT == kT2 ? (size_t)(K >> 7) * N * 2 : wrows * gpr * 2));
 
   // ---- per-lane B source: NB columns (16 apart) ----
   const int bcol = lane & 15;
   const int bblk = lane >> 4;
   int ncol[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) ncol[nb] = nw0 + nb * 16 + bcol;  // columns past N read zeros, are not stored
+  for (int nb = 0; nb < NB; ++nb) {  // columns past N read zeros and are not stored
+    if constexpr (MODE == kGroupedSwiglu)
+      ncol[nb] = nb < NB / 2 ? nw0 + nb * 16 + bcol : ga.F + nw0 + (nb - NB / 2) * 16 + bcol;
+    else
+      ncol[nb] = nw0 + nb * 16 + bcol;
+    if (MODE == kGroupedSwiglu && nw0 + (nb % (NB / 2)) * 16 + bcol >= ga.F) ncol[nb] = N;  // past F: invalid
+  }
+  const uint32_t wrow0 = (uint32_t)expert * (uint32_t)ga.n_per_expert;  // first W row of this tile's expert
 
   auto load_b = [&](int ks, uint4 (&wv)[NB], float (&sc)[NB][G32 ? 1 : 4]) {
     const int k = ks * kSuper + 32 * bblk;
@@ -145,15 +186,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, co
         wv[nb].z = wv[nb].w = 0;
         sc[nb][0] = buf_load_half(s_rsrc, ok ? ((uint32_t)(k >> 7) * N + n) * 2 : kOOB);
       } else {
-        const uint32_t row = (uint32_t)n * kw * 4;
+        const uint32_t wrow = wrow0 + (uint32_t)n;
+        const uint32_t row = wrow * kw * 4;
         wv[nb] = buf_load16(w_rsrc, ok ? row + (uint32_t)(k >> 3) * 4 : kOOB);
         if constexpr (G32) {
-          sc[nb][0] = buf_load_half(s_rsrc, ok ? (uint32_t)n * gpr * 2 + (uint32_t)(k / group) * 2 : kOOB);
+          sc[nb][0] = buf_load_half(s_rsrc, ok ? wrow * gpr * 2 + (uint32_t)(k / group) * 2 : kOOB);
         } else {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            sc[nb][j] = buf_load_half(s_rsrc, ok ? (uint32_t)n * gpr * 2 + (uint32_t)((k + 8 * j) / group) * 2
-                                                 : kOOB);
+            sc[nb][j] = buf_load_half(s_rsrc, ok ? wrow * gpr * 2 + (uint32_t)((k + 8 * j) / group) * 2 : kOOB);
         }
       }
     }
@@ -183,15 +224,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, co
   };
 
   // ---- X staging: unit u = t + 256 i: row r = u / UPR, k offset ku * (16 or 8) ----
+  // X row of each staging unit (fixed for the whole K loop): the tile row, or its token through src
+  int xrow[UPT];
+#pragma unroll
+  for (int i = 0; i < UPT; ++i) {
+    const int u = threadIdx.x + 256 * i;
+    const int g = m0 + u / UPR;
+    int m = g;
+    if constexpr (MODE != kDense) m = g < ga.rows_total ? (ga.src ? ga.src[g] : g) : -1;
+    xrow[i] = ((UNITS % 256 == 0 || u < UNITS) && m >= 0 && m < M) ? m : -1;
+  }
   auto load_x = [&](int ks, uint4 (&xr)[UPT][UL]) {
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       const int u = threadIdx.x + 256 * i;
-      const int r = u / UPR;
       const int ku = u % UPR;
-      const int m = m0 + r;
+      const int m = xrow[i];
       const int k = ks * kSuper + ku * (FMT == kT2 ? 16 : 8);
-      const bool ok = (UNITS % 256 == 0 || u < UNITS) && m < M && k < K;
+      const bool ok = m >= 0 && k < K;
       const uint32_t e = ((uint32_t)m * K + k) * (XF32 ? 4 : 2);  // byte offset
 #pragma unroll
       for (int q = 0; q < UL; ++q) xr[i][q] = buf_load16(xr_rsrc, ok ? e + 16 * q : kOOB);
@@ -289,22 +339,43 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const void* __restrict__ xv, co
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows past M ----
-  float* out = SPLIT ? part + (size_t)sp * M * N : y;
-  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(out, (uint32_t)((size_t)M * N * 4));
+  // ---- epilogue: lane holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows past the end ----
   const int rq = (lane >> 4) * 4;
+  if constexpr (MODE == kGroupedSwiglu) {
+    const int F = ga.F;
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(ga.act, (uint32_t)((size_t)ga.rows_total * F * 2));
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int n = nw0 + nb * 16 + bcol;
+    for (int nb = 0; nb < NB / 2; ++nb) {
+      const int j = nw0 + nb * 16 + bcol;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + mb * 16 + rq + r;
-        const uint32_t off = n < N ? ((uint32_t)m * N + n) * 4 : kOOB;
-        float v = acc[mb][nb][r];
-        if constexpr (ADD && !SPLIT) v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+        for (int r = 0; r < 4; ++r) {
+          const int g = m0 + mb * 16 + rq + r;
+          const uint32_t off = j < F ? ((uint32_t)g * F + j) * 2 : kOOB;
+          const float v = silu(acc[mb][nb][r]) * acc[mb][nb + NB / 2][r];
+          __builtin_amdgcn_raw_buffer_store_b16(float_to_half_bits(v), a_rsrc, off, 0, 0);
+        }
+      }
+    }
+  } else {
+    const int rows_out = MODE == kDense ? M : ga.rows_total;
+    float* out = SPLIT ? part + (size_t)sp * M * N : y;
+    const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(out, (uint32_t)((size_t)rows_out * N * 4));
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n = nw0 + nb * 16 + bcol;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + mb * 16 + rq + r;
+          const uint32_t off = n < N ? ((uint32_t)m * N + n) * 4 : kOOB;
+          float v = acc[mb][nb][r];
+          if constexpr (ADD && !SPLIT)
+            v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+        }
       }
     }
   }
@@ -363,7 +434,7 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
                        int K, int group, const GemmPlan& p, hipStream_t s) {
   constexpr int NB = 4;
   const size_t lds = 2 * (size_t)MB * 256 * 16;
-  auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT>;
+  auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT, kDense>;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
@@ -371,8 +442,11 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
   }
   int blocks = p.mtiles * p.ntiles * p.splits;
   blocks = (blocks + 7) / 8 * 8;  // extra workgroups exit at once; a multiple of 8 enables the XCD mapping
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, x, wq, ws, y, part, M, N, K, group, p.mtiles, p.ntiles,
-                     p.splits, p.sup_per_split);
+  GemmArgs ga{};
+  ga.x = x; ga.w = wq; ga.s = ws; ga.y = y; ga.part = part;
+  ga.M = M; ga.N = N; ga.K = K; ga.group = group; ga.mtiles = p.mtiles; ga.ntiles = p.ntiles;
+  ga.splits = p.splits; ga.sup_per_split = p.sup_per_split;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();
 }
 
@@ -435,6 +509,77 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
              : gemm_dispatch<FMT, false, false>(x, wq, ws, y, part, M, N, K, group, add, p, s);
 }
 
+// ---- grouped (MoE) GEMM ----------------------------------------------------------------------------------------
+template <int MB, bool G32, bool XF32, int MODE>
+static int launch_grouped(const GemmArgs& ga0, int max_tiles, hipStream_t s) {
+  constexpr int NB = 4;
+  const size_t lds = 2 * (size_t)MB * 256 * 16;
+  auto kern = k_gemm<kQ4, MB, NB, G32, XF32, false, false, MODE>;
+  GemmArgs ga = ga0;
+  ga.ntiles = MODE == kGroupedSwiglu ? (ga.F + 2 * 16 * NB - 1) / (2 * 16 * NB) : (ga.N + 64 * NB - 1) / (64 * NB);
+  ga.splits = 1;
+  ga.sup_per_split = (ga.K + kSuper - 1) / kSuper;
+  const int blocks = ga.ntiles * max_tiles;
+  if (blocks <= 0) return AQ_OK;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
+  return launch_status();
+}
+
+template <bool G32, bool XF32, int MODE>
+static int grouped_mb(const GemmArgs& ga, int mb, int max_tiles, hipStream_t s) {
+  switch (mb) {
+    case 1: return launch_grouped<1, G32, XF32, MODE>(ga, max_tiles, s);
+    case 2: return launch_grouped<2, G32, XF32, MODE>(ga, max_tiles, s);
+    case 3: return launch_grouped<3, G32, XF32, MODE>(ga, max_tiles, s);
+    case 4: return launch_grouped<4, G32, XF32, MODE>(ga, max_tiles, s);
+    case 5: return launch_grouped<5, G32, XF32, MODE>(ga, max_tiles, s);
+    case 6: return launch_grouped<6, G32, XF32, MODE>(ga, max_tiles, s);
+    default: return launch_grouped<7, G32, XF32, MODE>(ga, max_tiles, s);
+  }
+}
+
+}  // namespace aq
+
+// Grouped int4 GEMM over experts (see include/aq.h).
+extern "C" int aq_moe_gemm_q4(const void* x, int32_t x_is_f32, int64_t x_rows, const int32_t* src,
+                              const uint32_t* wq, const uint16_t* ws, int64_t experts, int64_t n, int64_t k,
+                              int32_t group, const int32_t* tiles, const int32_t* ntiles, int32_t max_tiles,
+                              int32_t tm, int64_t rows_total, int32_t swiglu, void* out, void* stream) {
+  using namespace aq;
+  if (!x || !wq || !ws || !tiles || !ntiles || !out) return AQ_ERR_NULL;
+  if (x_rows <= 0 || experts <= 0 || n <= 0 || k <= 0 || k % 32 || max_tiles < 0 || rows_total <= 0)
+    return AQ_ERR_SHAPE;
+  if (tm % 16 || tm < 16 || tm > 16 * kMaxMB) return AQ_ERR_SHAPE;
+  if (swiglu && n % 2) return AQ_ERR_SHAPE;
+  if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
+  if (experts * n * k / 2 >= ((int64_t)1 << 31) || x_rows * k * (x_is_f32 ? 4 : 2) >= ((int64_t)1 << 31) ||
+      rows_total * n * 4 >= ((int64_t)1 << 31))
+    return AQ_ERR_CAPACITY;
+  if (!aligned(wq, 16) || !aligned(x, 16)) return AQ_ERR_ALIGN;
+  GemmArgs ga{};
+  ga.x = x; ga.w = wq; ga.s = ws;
+  ga.y = static_cast<float*>(out);
+  ga.act = static_cast<uint16_t*>(out);
+  ga.tiles = tiles; ga.ntiles_dev = ntiles; ga.src = src;
+  ga.M = (int)x_rows; ga.N = (int)n; ga.K = (int)k; ga.group = group;
+  ga.mtiles = (int)experts;  // grouped launches keep the expert count here (W rows = experts * n)
+  ga.n_per_expert = (int)n; ga.F = (int)(n / 2); ga.rows_total = (int)rows_total;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int mb = tm / 16;
+  const bool g32 = group % 32 == 0;
+  if (swiglu) {
+    if (x_is_f32) return g32 ? grouped_mb<true, true, kGroupedSwiglu>(ga, mb, max_tiles, st)
+                             : grouped_mb<false, true, kGroupedSwiglu>(ga, mb, max_tiles, st);
+    return g32 ? grouped_mb<true, false, kGroupedSwiglu>(ga, mb, max_tiles, st)
+               : grouped_mb<false, false, kGroupedSwiglu>(ga, mb, max_tiles, st);
+  }
+  if (x_is_f32) return g32 ? grouped_mb<true, true, kGrouped>(ga, mb, max_tiles, st)
+                           : grouped_mb<false, true, kGrouped>(ga, mb, max_tiles, st);
+  return g32 ? grouped_mb<true, false, kGrouped>(ga, mb, max_tiles, st)
+             : grouped_mb<false, false, kGrouped>(ga, mb, max_tiles, st);
+}
+
+namespace aq {
 }  // namespace aq
 
 extern "C" int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y,

@@ -1,0 +1,429 @@
+// Mixture-of-experts plumbing around the grouped int4 GEMM, gfx950: top-k routing, deterministic expert grouping
+// (histogram, padded prefix sum, stable permute, work tiles), the weighted combine, the decode-time expert GEMVs and
+// the fp32 router GEMV.
+//
+// Reference: qwen3moe/kernels/moek.mojo (route :156-197, p_route :385-425, moe_gate_up :200-210, moe_down :213-223,
+// gemv_f32 :143-153, p_expert_lists :432-442, p_expert_items :548-557, p_moe_sum :479-488) and
+// lfm2moe/kernels/mk.mojo (p_group :123-161, p_combine :189-199). Every index this file produces is a pure function
+// of the routing ids (no atomics decide an order), so routing, lists, slots and tiles are bit-for-bit reproducible.
+#include "aq_common.h"
+
+namespace aq {
+
+// ---- routing: top-k of E logits per token, lowest index among equals; weights = softmax over the k winners ----
+// One wave per token. Each lane holds E/64 (<= 4) logits; k rounds of a (value, index) wave arg-max.
+template <int PER_LANE>
+__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int32_t* __restrict__ ids,
+                                               float* __restrict__ weights, int tokens, int E, int topk) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  float v[PER_LANE];
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
+  }
+  float top[8];
+  for (int k = 0; k < topk; ++k) {
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && (v[j] > best || (v[j] == best && e < bi))) {
+        best = v[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ob = __shfl_xor(best, m, 64);
+      const int oi = __shfl_xor(bi, m, 64);
+      if (ob > best || (ob == best && oi < bi)) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    top[k] = best;
+    if (lane == 0) ids[(size_t)t * topk + k] = bi;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j)
+      if (lane + 64 * j == bi) v[j] = -INFINITY;
+  }
+  if (lane == 0) {
+    float total = 0.f;
+    for (int k = 0; k < topk; ++k) total += expf(top[k] - top[0]);
+    for (int k = 0; k < topk; ++k) weights[(size_t)t * topk + k] = expf(top[k] - top[0]) / total;
+  }
+}
+
+// ---- grouping: one 1024-thread workgroup --------------------------------------------------------------------------
+// Entry i = t * topk + k chose expert ids[i]. Per expert e: cnt[e] entries; segments in expert order, each padded to
+// a multiple of tm rows, start at offs[e] (exclusive prefix sum of the padded counts); entry i's row slot[i] is
+// offs[e] + its rank among e's entries in ascending i; src[row] = its token (-1 on padding rows); work tiles
+// (e, offs[e] + c) for c = 0, tm, ... < cnt[e], in expert order, and their number. Optionally the qwen3moe lists
+// (lists[e * cap + r] = i of rank r) and items ((e, c) every `items_tt` entries).
+// Thread (e, q) for q < Q = 1024 / E scans the q-th contiguous segment of the entries, so counting and placing stay
+// in entry order without atomics.
+struct GroupOut {
+  int32_t* counts;   // [E]
+  int32_t* offs;     // [E + 1]
+  int32_t* slot;     // [n]
+  int32_t* src;      // [max_rows]
+  int32_t* tiles;    // [2 * max_tiles]
+  int32_t* ntiles;   // [1]
+  int32_t* lists;    // [E * cap] or null
+  int32_t* items;    // [2 * max_items] or null
+  int32_t* nitems;   // [1] or null
+  int cap, items_tt, max_rows, max_tiles, max_items;
+};
+
+__global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int n, int topk, int E, int tm,
+                                                    GroupOut o) {
+  extern __shared__ int32_t sm[];
+  int32_t* sid = sm;                 // [n] ids
+  int32_t* cnt = sid + n;            // [E][Q] segment counts, then segment start rows
+  const int Q = max(1, 1024 / E);
+  int32_t* ecount = cnt + E * Q;     // [E]
+  int32_t* eoff = ecount + E;        // [E + 1]
+  int32_t* tbase = eoff + E + 1;     // [E + 1] first tile of each expert
+  int32_t* ibase = tbase + E + 1;    // [E + 1] first item of each expert
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    sid[i] = ids[i];
+    o.slot[i] = -1;  // stays -1 for an id outside [0, E): such an entry is in no group
+  }
+  __syncthreads();
+  const int seg = (n + Q - 1) / Q;
+  for (int w = threadIdx.x; w < E * Q; w += 1024) {
+    const int e = w / Q, q = w - e * Q;
+    const int i0 = q * seg, i1 = min(n, i0 + seg);
+    int c = 0;
+    for (int i = i0; i < i1; ++i) c += sid[i] == e;
+    cnt[w] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
+    int c = 0;
+    for (int q = 0; q < Q; ++q) c += cnt[e * Q + q];
+    ecount[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // prefix sums over experts (E <= 1024 values)
+    int off = 0, tb = 0, ib = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = ecount[e];
+      eoff[e] = off;
+      tbase[e] = tb;
+      ibase[e] = ib;
+      off += (c + tm - 1) / tm * tm;
+      tb += (c + tm - 1) / tm;
+      if (o.items) ib += (c + o.items_tt - 1) / o.items_tt;
+    }
+    eoff[E] = off;
+    tbase[E] = tb;
+    ibase[E] = ib;
+    o.ntiles[0] = tb;
+    if (o.nitems) o.nitems[0] = ib;
+    o.offs[E] = off;
+  }
+  __syncthreads();
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
+    const int c = ecount[e];
+    o.counts[e] = c;
+    o.offs[e] = eoff[e];
+    int start = eoff[e];
+    for (int q = 0; q < Q; ++q) {  // segment start rows
+      const int cq = cnt[e * Q + q];
+      cnt[e * Q + q] = start;
+      start += cq;
+    }
+    const int pad_end = eoff[e] + (c + tm - 1) / tm * tm;
+    for (int r = eoff[e] + c; r < pad_end && r < o.max_rows; ++r) o.src[r] = -1;
+    for (int j = 0, t0 = 0; t0 < c; ++j, t0 += tm) {
+      if (tbase[e] + j < o.max_tiles) {
+        o.tiles[2 * (tbase[e] + j)] = e;
+        o.tiles[2 * (tbase[e] + j) + 1] = eoff[e] + t0;
+      }
+    }
+    if (o.items)
+      for (int j = 0, t0 = 0; t0 < c; ++j, t0 += o.items_tt)
+        if (ibase[e] + j < o.max_items) {
+          o.items[2 * (ibase[e] + j)] = e;
+          o.items[2 * (ibase[e] + j) + 1] = t0;
+        }
+  }
+  __syncthreads();
+  for (int w = threadIdx.x; w < E * Q; w += 1024) {
+    const int e = w / Q, q = w - e * Q;
+    const int i0 = q * seg, i1 = min(n, i0 + seg);
+    int row = cnt[w];
+    for (int i = i0; i < i1; ++i) {
+      if (sid[i] == e) {
+        o.slot[i] = row;
+        if (row < o.max_rows) o.src[row] = i / topk;
+        if (o.lists) o.lists[(size_t)e * o.cap + (row - eoff[e])] = i;
+        ++row;
+      }
+    }
+  }
+  // rows past the last segment are never in a tile; mark them padding too
+  for (int r = eoff[E] + threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;
+}
+
+// ---- combine: y[t, c] = (add ? y[t, c] : 0) + sum_k w[t, k] * yd[slot[t*topk + k], c], k in order ----
+__global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ yd, const int32_t* __restrict__ slot,
+                                                     const float* __restrict__ w, float* __restrict__ y, int tokens,
+                                                     int d, int topk, int add, int yd_rows) {
+  const int d4 = d >> 2;
+  const int64_t total = (int64_t)tokens * d4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int t = (int)(i / d4);
+    const int c = (int)(i - (int64_t)t * d4);
+    float4 acc = add ? reinterpret_cast<const float4*>(y + (size_t)t * d)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < topk; ++k) {
+      const int r = slot ? slot[t * topk + k] : t * topk + k;
+      if (r < 0 || r >= yd_rows) continue;  // an entry in no group contributes nothing
+      const float wk = w[t * topk + k];
+      const float4 v = reinterpret_cast<const float4*>(yd + (size_t)r * d)[c];
+      acc.x = fmaf(wk, v.x, acc.x);
+      acc.y = fmaf(wk, v.y, acc.y);
+      acc.z = fmaf(wk, v.z, acc.z);
+      acc.w = fmaf(wk, v.w, acc.w);
+    }
+    reinterpret_cast<float4*>(y + (size_t)t * d)[c] = acc;
+  }
+}
+
+// ---- decode-time expert GEMVs (one token) ----
+// Lane share of W[row] . xs over K (x in LDS), 16-byte chunks c = lane, lane + 64, ...; G a multiple of 8.
+__device__ __forceinline__ float row_dot_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                                            size_t row, int K, int group, const float* xs, int lane) {
+  const int kw = K >> 3;
+  const int gpr = K / group;
+  float acc = 0.f;
+  for (int c = lane; c < (K >> 5); c += 64) {
+    const uint4 w4 = *reinterpret_cast<const uint4*>(wq + row * kw + c * 4);
+    const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float* xv = xs + c * 32 + j * 8;
+      const float xsum = ((xv[0] + xv[1]) + (xv[2] + xv[3])) + ((xv[4] + xv[5]) + (xv[6] + xv[7]));
+      const float sc = half_bits_to_float(ws[row * gpr + (c * 32 + j * 8) / group]);
+      acc = fmaf(dot8_biased(wv[j], xv) - 8.0f * xsum, sc, acc);
+    }
+  }
+  return acc;
+}
+
+// a[e, j] = silu(W[ids[e] * 2F + j] . x) * (W[ids[e] * 2F + F + j] . x): one wave per (e, j).
+__global__ __launch_bounds__(256) void k_moe_gate_up(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                                                     const int32_t* __restrict__ ids, const float* __restrict__ x,
+                                                     float* __restrict__ a, int F, int K, int group, int topk,
+                                                     int experts) {
+  extern __shared__ float xs[];
+  for (int i = threadIdx.x; i < K; i += 256) xs[i] = x[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o >= topk * F) return;
+  const int e = o / F, j = o - e * F;
+  const int ex = ids[e];
+  if (ex < 0 || ex >= experts) {  // an invalid id selects no weights
+    if (lane == 0) a[(size_t)e * F + j] = 0.f;
+    return;
+  }
+  const size_t row = (size_t)ex * 2 * F + j;
+  const float g = wave_sum(row_dot_q4(wq, ws, row, K, group, xs, lane));
+  const float u = wave_sum(row_dot_q4(wq, ws, row + F, K, group, xs, lane));
+  if (lane == 0) a[(size_t)e * F + j] = silu(g) * u;
+}
+
+// y[r] (+)= sum_e weights[e] * W[ids[e] * D + r] . a[e] (e in order): one wave per output row.
+__global__ __launch_bounds__(256) void k_moe_down(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                                                  const int32_t* __restrict__ ids, const float* __restrict__ weights,
+                                                  const float* __restrict__ a, float* __restrict__ y, int D, int F,
+                                                  int group, int topk, int add, int experts) {
+  extern __shared__ float as[];
+  for (int i = threadIdx.x; i < topk * F; i += 256) as[i] = a[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= D) return;
+  float acc = 0.f;
+  for (int e = 0; e < topk; ++e) {
+    const int ex = ids[e];
+    if (ex < 0 || ex >= experts) continue;  // wave-uniform: an invalid id contributes nothing
+    acc = fmaf(weights[e], wave_sum(row_dot_q4(wq, ws, (size_t)ex * D + r, F, group, as + e * F, lane)), acc);
+  }
+  if (lane == 0) y[r] = add ? y[r] + acc : acc;
+}
+
+// ---- router: y[t, r] = W[r] . x[t] with fp32 W: one wave per (row, token) ----
+__global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ w, const float* __restrict__ x,
+                                                  float* __restrict__ y, int n, int k, int tokens) {
+  const int lane = threadIdx.x & 63;
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o >= n * tokens) return;
+  const int t = o / n, r = o - t * n;
+  const float* wr = w + (size_t)r * k;
+  const float* xr = x + (size_t)t * k;
+  float acc = 0.f;
+  if ((k & 3) == 0) {
+    for (int c = lane; c < (k >> 2); c += 64) {
+      const float4 a = reinterpret_cast<const float4*>(wr)[c];
+      const float4 b = reinterpret_cast<const float4*>(xr)[c];
+      acc = fmaf(a.x, b.x, fmaf(a.y, b.y, fmaf(a.z, b.z, fmaf(a.w, b.w, acc))));
+    }
+  } else {
+    for (int c = lane; c < k; c += 64) acc = fmaf(wr[c], xr[c], acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[(size_t)t * n + r] = acc;
+}
+
+}  // namespace aq
+
+using namespace aq;
+
+extern "C" int aq_moe_route(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts,
+                            int32_t topk, void* stream) {
+  if (!logits || !ids || !weights) return AQ_ERR_NULL;
+  if (tokens <= 0 || experts <= 0 || experts > 256 || topk <= 0 || topk > 8 || topk > experts) return AQ_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((tokens + 3) / 4));
+  if (experts <= 64)
+    hipLaunchKernelGGL(k_route<1>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
+  else if (experts <= 128)
+    hipLaunchKernelGGL(k_route<2>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
+  else
+    hipLaunchKernelGGL(k_route<4>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
+  return launch_status();
+}
+
+extern "C" int64_t aq_moe_group_max_rows(int64_t tokens, int32_t topk, int32_t experts, int32_t tm) {
+  if (tokens <= 0 || topk <= 0 || experts <= 0 || tm <= 0) return 0;
+  return (tokens * topk + (int64_t)experts * (tm - 1) + tm - 1) / tm * tm;
+}
+
+extern "C" int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t experts, int32_t tm) {
+  if (tokens <= 0 || topk <= 0 || experts <= 0 || tm <= 0) return 0;
+  return (int32_t)((tokens * topk + (int64_t)experts * (tm - 1)) / tm);
+}
+
+static size_t group_lds(int64_t n, int E) {
+  const int Q = E >= 1024 ? 1 : 1024 / E;
+  return (size_t)(n + (int64_t)E * Q + 4 * (E + 1)) * 4;
+}
+
+extern "C" int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm,
+                            int32_t* counts, int32_t* offs, int32_t* slot, int32_t* src, int64_t max_rows,
+                            int32_t* tiles, int32_t max_tiles, int32_t* ntiles, void* stream) {
+  if (!ids || !counts || !offs || !slot || !src || !tiles || !ntiles) return AQ_ERR_NULL;
+  if (tokens <= 0 || topk <= 0 || experts <= 0 || experts > 1024 || tm <= 0) return AQ_ERR_SHAPE;
+  if (max_rows < aq_moe_group_max_rows(tokens, topk, experts, tm) ||
+      max_tiles < aq_moe_group_max_tiles(tokens, topk, experts, tm))
+    return AQ_ERR_CAPACITY;
+  const int64_t n = tokens * topk;
+  const size_t lds = group_lds(n, experts);
+  if (lds > 160 * 1024) return AQ_ERR_CAPACITY;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_moe_group), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return AQ_ERR_CAPACITY;
+  GroupOut o{};
+  o.counts = counts; o.offs = offs; o.slot = slot; o.src = src; o.tiles = tiles; o.ntiles = ntiles;
+  o.max_rows = (int)max_rows; o.max_tiles = max_tiles;
+  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), lds, reinterpret_cast<hipStream_t>(stream), ids, (int)n, topk,
+                     experts, tm, o);
+  return launch_status();
+}
+
+extern "C" int aq_moe_expert_lists(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t cap,
+                                   int32_t* lists, int32_t* counts, int32_t items_tt, int32_t* items,
+                                   int32_t max_items, int32_t* nitems, int32_t* scratch, int64_t scratch_ints,
+                                   void* stream) {
+  if (!ids || !lists || !counts || !scratch) return AQ_ERR_NULL;
+  if (tokens <= 0 || topk <= 0 || experts <= 0 || experts > 1024 || cap < tokens) return AQ_ERR_SHAPE;
+  if (items && (items_tt <= 0 || !nitems)) return AQ_ERR_ARG;
+  const int64_t n = tokens * topk;
+  // the lists are the grouping with tm = 1 (no padding); its offsets, slots, src and tiles go to the scratch ints
+  const int64_t need = (experts + 1) + n + n + 2 * n + 1;
+  if (scratch_ints < need) return AQ_ERR_CAPACITY;
+  const size_t lds = group_lds(n, experts);
+  if (lds > 160 * 1024) return AQ_ERR_CAPACITY;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_moe_group), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return AQ_ERR_CAPACITY;
+  GroupOut o{};
+  o.counts = counts;
+  o.offs = scratch;
+  o.slot = scratch + (experts + 1);
+  o.src = o.slot + n;
+  o.tiles = o.src + n;
+  o.ntiles = o.tiles + 2 * n;
+  o.max_rows = (int)n;
+  o.max_tiles = (int)n;
+  o.lists = lists;
+  o.cap = cap;
+  o.items = items;
+  o.items_tt = items_tt;
+  o.nitems = nitems;
+  o.max_items = max_items;
+  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), lds, reinterpret_cast<hipStream_t>(stream), ids, (int)n, topk,
+                     experts, 1, o);
+  return launch_status();
+}
+
+extern "C" int aq_moe_combine(const float* yd, int64_t yd_rows, const int32_t* slot, const float* weights, float* y,
+                              int64_t tokens, int64_t d, int32_t topk, int32_t add, void* stream) {
+  if (!yd || !weights || !y) return AQ_ERR_NULL;
+  if (tokens <= 0 || d <= 0 || d % 4 || topk <= 0 || yd_rows <= 0 || yd_rows > (1 << 30)) return AQ_ERR_SHAPE;
+  if (!aligned(yd, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
+  int64_t blocks = (tokens * d / 4 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), yd,
+                     slot, weights, y, (int)tokens, (int)d, topk, add, (int)yd_rows);
+  return launch_status();
+}
+
+extern "C" int aq_moe_gate_up_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids,
+                                 const float* x, float* a, int64_t f, int64_t k, int32_t group, int32_t topk,
+                                 void* stream) {
+  if (!wq || !ws || !ids || !x || !a) return AQ_ERR_NULL;
+  if (f <= 0 || k <= 0 || k % 32 || topk <= 0 || topk * f > (1 << 30) || experts <= 0) return AQ_ERR_SHAPE;
+  if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
+  if (k * 4 > 64 * 1024) return AQ_ERR_CAPACITY;
+  if (!aligned(wq, 16)) return AQ_ERR_ALIGN;
+  hipLaunchKernelGGL(k_moe_gate_up, dim3((unsigned)((topk * f + 3) / 4)), dim3(256), (size_t)k * 4,
+                     reinterpret_cast<hipStream_t>(stream), wq, ws, ids, x, a, (int)f, (int)k, group, topk,
+                     (int)experts);
+  return launch_status();
+}
+
+extern "C" int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids,
+                              const float* weights, const float* a, float* y, int64_t d, int64_t f, int32_t group,
+                              int32_t topk, int32_t add, void* stream) {
+  if (!wq || !ws || !ids || !weights || !a || !y) return AQ_ERR_NULL;
+  if (d <= 0 || f <= 0 || f % 32 || topk <= 0 || d > (1 << 30) || experts <= 0) return AQ_ERR_SHAPE;
+  if (group <= 0 || group % 8 || f % group) return AQ_ERR_GROUP;
+  if (topk * f * 4 > 64 * 1024) return AQ_ERR_CAPACITY;
+  if (!aligned(wq, 16)) return AQ_ERR_ALIGN;
+  hipLaunchKernelGGL(k_moe_down, dim3((unsigned)((d + 3) / 4)), dim3(256), (size_t)topk * f * 4,
+                     reinterpret_cast<hipStream_t>(stream), wq, ws, ids, weights, a, y, (int)d, (int)f, group, topk,
+                     add, (int)experts);
+  return launch_status();
+}
+
+extern "C" int aq_gemv_f32(const float* w, const float* x, float* y, int64_t n, int64_t k, int32_t tokens,
+                           void* stream) {
+  if (!w || !x || !y) return AQ_ERR_NULL;
+  if (n <= 0 || k <= 0 || tokens <= 0 || n * tokens > (1 << 30)) return AQ_ERR_SHAPE;
+  if ((k & 3) == 0 && (!aligned(w, 16) || !aligned(x, 16))) return AQ_ERR_ALIGN;
+  hipLaunchKernelGGL(k_gemv_f32, dim3((unsigned)((n * tokens + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w, x, y, (int)n, (int)k, tokens);
+  return launch_status();
+}

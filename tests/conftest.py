@@ -30,6 +30,7 @@ def dev():
     if not gpu_available():
         pytest.skip("no GPU visible")
     import torch
+    import aq  # noqa: F401  (registers torch.ops.aq.*)
     return torch.device("cuda:0")
 
 
