@@ -168,6 +168,87 @@ def bench_gemm_c1(dev, steps: int, warmup: int, layers: int = 16):
                 weights_mb=round(layers * sum(n * k * 0.5625 for _, n, k in C1_LAYER) / 1e6, 1))
 
 
+def _t2_gemv_bytes(n, k):
+    return (k // 16) * n * 4 + (k // 128) * n * 2 + k * 2 + n * 4
+
+
+C2_MATS = (("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288))
+
+
+def bench_ternary_c2(dev, pool_mb: int = 560):
+    """C2: ternary GEMV (M=1) over a rotating pool of distinct gate/up/down triples, and ternary GEMM at M=412."""
+    import numpy as np
+    import torch
+    from aq import ops, synth
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(102)
+    per_triple = sum(_t2_gemv_bytes(n, k) for _, n, k in C2_MATS)
+    copies = max(2, int(pool_mb * 1e6 // per_triple))
+    rng = np.random.default_rng(2)
+    mats = []
+    for c in range(copies):
+        trip = {}
+        for name, n, k in C2_MATS:
+            if c == 0:
+                w, s_ = synth.ternary_matrix(rng, n, k)
+                trip[name] = (_dev(w, dev), _dev(s_, dev))
+            else:  # random 2-bit codes (3 would decode to +2; timing does not depend on the values)
+                w = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 16, n), dtype=torch.int32, device=dev, generator=gen)
+                s_ = (torch.rand((k // 128, n), device=dev, generator=gen) * 0.02).to(torch.float16)
+                trip[name] = (w, s_)
+        mats.append(trip)
+    xh = {k: torch.randint(0, 2 ** 14, (k // 2,), dtype=torch.int32, device=dev, generator=gen) for k in (4096, 12288)}
+    ys = {name: torch.empty(n, dtype=torch.float32, device=dev) for name, n, _ in C2_MATS}
+    launches = [(lambda w=m[name][0], s_=m[name][1], k=k, y=ys[name]: ops.t2_gemv(xh[k], w, s_, y))
+                for m in mats for name, _, k in C2_MATS]
+    t_all = GraphTimer(launches).time(replays=3)
+    gemv = dict(gbs=round(copies * per_triple / t_all / 1e9, 2), us_per_triple=round(t_all / copies * 1e6, 3),
+                frac_hbm=round(copies * per_triple / t_all / 1e9 / HBM_PEAK_GBS, 4), pool_mb=round(copies * per_triple / 1e6, 1))
+    m = synth.C2_GEMM_TOKENS
+    xs = {k: torch.randn((m, k), device=dev, generator=gen).to(torch.float16) for k in (4096, 12288)}
+    yg = {name: torch.empty((m, n), dtype=torch.float32, device=dev) for name, n, _ in C2_MATS}
+    gl = [(lambda w=mm[name][0], s_=mm[name][1], k=k, y=yg[name]: ops.gemm_t2(xs[k], w, s_, y))
+          for mm in mats[:4] for name, _, k in C2_MATS]
+    t_g = GraphTimer(gl).time(replays=3) / min(4, copies)
+    flop = sum(2 * m * n * k for _, n, k in C2_MATS)
+    gemm = dict(tflops=round(flop / t_g / 1e12, 2), us_per_triple=round(t_g * 1e6, 3),
+                frac_mfma=round(flop / t_g / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), tokens=m)
+    return dict(gemv=gemv, gemm=gemm)
+
+
+def bench_moe_c3(dev):
+    """C3: Qwen3-30B-A3B-shaped MoE block at 404 tokens (grouped prefill) and at 1 token (decode), over two distinct
+    expert weight sets (2 x 340 MB) alternating, so the 256 MB Infinity Cache cannot hold them."""
+    import numpy as np
+    import torch
+    from aq import moe, synth
+    d = synth.c3()
+    sets = []
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(103)
+    for c in range(2):
+        if c == 0:
+            w = [_dev(d[kk], dev) for kk in ("gu_q", "gu_s", "dn_q", "dn_s")]
+        else:
+            w = [torch.randint(-2 ** 31, 2 ** 31 - 1, t.shape, dtype=torch.int32, device=dev, generator=gen)
+                 if t.dtype == torch.int32 else (torch.rand(t.shape, device=dev, generator=gen) * 0.03 + 1e-3).half()
+                 for t in sets[0]._w]
+        blk = moe.MoeBlock(*w, 128, 2048, 768, 32, 8, max_tokens=404, tm=32)
+        blk._w = w
+        sets.append(blk)
+    x = _dev(d["x"], dev)
+    logits = _dev(d["logits"], dev)
+    out = torch.empty((404, 2048), dtype=torch.float32, device=dev)
+    t404 = GraphTimer([lambda b=b: b.forward(x, logits, out) for b in sets]).time(replays=5) / 2
+    x1, l1 = x[0].contiguous(), logits[0].contiguous()
+    o1 = torch.empty(2048, dtype=torch.float32, device=dev)
+    t1 = GraphTimer([lambda b=b: b.decode(x1, l1, o1) for b in sets]).time(replays=20) / 2
+    wbytes = 128 * (1536 * 2048 + 2048 * 768) * 0.5625
+    return dict(ms_404=round(t404 * 1e3, 4), ms_1=round(t1 * 1e3, 4),
+                gbs_404_weights=round(wbytes / t404 / 1e9, 1),
+                gbs_1_active=round(8 * (1536 * 2048 + 2048 * 768) * 0.5625 / t1 / 1e9, 1))
+
+
 def cpu_baseline_gemm():
     import numpy as np
     from aq import synth
@@ -216,6 +297,8 @@ def main():
     c1 = bench_gemm_c1(dev, args.steps, args.warmup)
     wall = time.perf_counter() - t0
     r = bench_gemv_c0(dev, 128, 10)
+    c2 = bench_ternary_c2(dev)
+    c3 = bench_moe_c3(dev)
     value = c1["flop"] / c1["t_step"] / 1e12
     gemv = r["bytes"] / r["t_burst"] / 1e9
     out = {
@@ -233,6 +316,8 @@ def main():
                     "gbs_single_cold": round(r["bytes"] / r["t_cold"] / 1e9, 2),
                     "us_burst": round(r["t_burst"] * 1e6, 3), "us_single_cold": round(r["t_cold"] * 1e6, 3),
                     "pool_mb": r["pool_mb"]},
+        "ternary_c2": c2,
+        "moe_c3": c3,
         "wall_s": round(wall, 2),
     }
     if not args.skip_cpu:

@@ -145,10 +145,9 @@ int aq_gemv_f32(const float* w, const float* x, float* y, int64_t n, int64_t k, 
 /* ---- ternary (T2W) matrix-vector products, decode ---------------------------------------------------------------
  * y[n] = sum_k (code(k, n) - 1) * s[k/128, n] * x[k], x as X2H fp16 pairs [K/2], T2W w [K/16, N], s fp16 [K/128, N],
  * fp32 accumulation (the reference accumulates groups in fp16). Requires K % 128 == 0, 16-byte aligned w.
- * Replaces: packed_linear + packed_reduce (bonsai/kernels/kernels.mojo:283-325,437-448) in one launch.
- * workspace: aq_t2_gemv_workspace_bytes(n, k) bytes, zero-filled before its first use: its first 64 KiB hold
- * per-column-tile arrival counters (every call leaves them at zero again), the rest split-K partials. Keep it for
- * aq_t2_gemv only; calls sharing it must be ordered on one stream. NULL runs without splitting K. */
+ * Replaces: packed_linear + packed_reduce (bonsai/kernels/kernels.mojo:283-325,437-448) in one launch: each workgroup
+ * owns a block of columns over all of K and reduces inside itself, so no cross-workgroup step is needed. K <= 32768.
+ * workspace is unused (aq_t2_gemv_workspace_bytes returns 0); it is kept in the signature for callers that pass one. */
 int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int64_t n, int64_t k,
                void* workspace, int64_t workspace_bytes, void* stream);
 int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);

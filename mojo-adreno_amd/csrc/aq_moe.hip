@@ -1,6 +1,6 @@
 // Mixture-of-experts plumbing around the grouped int4 GEMM, gfx950: top-k routing, deterministic expert grouping
-// (histogram, padded prefix sum, stable permute, work tiles), the weighted combine, the decode-time expert GEMVs and
-// the fp32 router GEMV.
+// (histogram, padded prefix sum, stable permute, work tiles), the weighted combine and the fp32 router GEMV. The
+// decode-time expert GEMVs are modes of the int4 GEMV (aq_gemv.hip).
 //
 // Reference: qwen3moe/kernels/moek.mojo (route :156-197, p_route :385-425, moe_gate_up :200-210, moe_down :213-223,
 // gemv_f32 :143-153, p_expert_lists :432-442, p_expert_items :548-557, p_moe_sum :479-488) and
@@ -64,8 +64,9 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
 // offs[e] + its rank among e's entries in ascending i; src[row] = its token (-1 on padding rows); work tiles
 // (e, offs[e] + c) for c = 0, tm, ... < cnt[e], in expert order, and their number. Optionally the qwen3moe lists
 // (lists[e * cap + r] = i of rank r) and items ((e, c) every `items_tt` entries).
-// Thread (e, q) for q < Q = 1024 / E scans the q-th contiguous segment of the entries, so counting and placing stay
-// in entry order without atomics.
+// Ranks without atomics deciding any order: bit t of expert e's token bitmap is set (LDS atomic OR, order-free) when
+// token t chose e; a token chooses an expert at most once (top-k of distinct experts), so the rank of entry i is the
+// number of set bits below t: a per-word prefix popcount plus the popcount of the bits below t in its word.
 struct GroupOut {
   int32_t* counts;   // [E]
   int32_t* offs;     // [E + 1]
@@ -81,36 +82,35 @@ struct GroupOut {
 
 __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int n, int topk, int E, int tm,
                                                     GroupOut o) {
-  extern __shared__ int32_t sm[];
-  int32_t* sid = sm;                 // [n] ids
-  int32_t* cnt = sid + n;            // [E][Q] segment counts, then segment start rows
-  const int Q = max(1, 1024 / E);
-  int32_t* ecount = cnt + E * Q;     // [E]
+  extern __shared__ unsigned long long bits[];  // [E][W] token bitmaps
+  const int T = n / topk;
+  const int W = (T + 63) >> 6;
+  int32_t* pre = reinterpret_cast<int32_t*>(bits + (size_t)E * W);  // [E][W] set bits before each word
+  int32_t* ecount = pre + E * W;     // [E]
   int32_t* eoff = ecount + E;        // [E + 1]
-  int32_t* tbase = eoff + E + 1;     // [E + 1] first tile of each expert
-  int32_t* ibase = tbase + E + 1;    // [E + 1] first item of each expert
+  int32_t* tbase = eoff + E + 1;     // [E + 1]
+  int32_t* ibase = tbase + E + 1;    // [E + 1]
+  for (int i = threadIdx.x; i < E * W; i += 1024) bits[i] = 0ull;
+  __syncthreads();
   for (int i = threadIdx.x; i < n; i += 1024) {
-    sid[i] = ids[i];
+    const int e = ids[i];
     o.slot[i] = -1;  // stays -1 for an id outside [0, E): such an entry is in no group
+    if (e >= 0 && e < E) {
+      const int t = i / topk;
+      atomicOr(&bits[(size_t)e * W + (t >> 6)], 1ull << (t & 63));
+    }
   }
   __syncthreads();
-  const int seg = (n + Q - 1) / Q;
-  for (int w = threadIdx.x; w < E * Q; w += 1024) {
-    const int e = w / Q, q = w - e * Q;
-    const int i0 = q * seg, i1 = min(n, i0 + seg);
-    int c = 0;
-    for (int i = i0; i < i1; ++i) c += sid[i] == e;
-    cnt[w] = c;
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int run = 0;
+    for (int w = 0; w < W; ++w) {
+      pre[e * W + w] = run;
+      run += __popcll(bits[(size_t)e * W + w]);
+    }
+    ecount[e] = run;
   }
   __syncthreads();
-  if (threadIdx.x < E) {
-    const int e = threadIdx.x;
-    int c = 0;
-    for (int q = 0; q < Q; ++q) c += cnt[e * Q + q];
-    ecount[e] = c;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {  // prefix sums over experts (E <= 1024 values)
+  if (threadIdx.x == 0) {  // prefix sums over experts
     int off = 0, tb = 0, ib = 0;
     for (int e = 0; e < E; ++e) {
       const int c = ecount[e];
@@ -129,17 +129,10 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
     o.offs[E] = off;
   }
   __syncthreads();
-  if (threadIdx.x < E) {
-    const int e = threadIdx.x;
+  for (int e = threadIdx.x; e < E; e += 1024) {
     const int c = ecount[e];
     o.counts[e] = c;
     o.offs[e] = eoff[e];
-    int start = eoff[e];
-    for (int q = 0; q < Q; ++q) {  // segment start rows
-      const int cq = cnt[e * Q + q];
-      cnt[e * Q + q] = start;
-      start += cq;
-    }
     const int pad_end = eoff[e] + (c + tm - 1) / tm * tm;
     for (int r = eoff[e] + c; r < pad_end && r < o.max_rows; ++r) o.src[r] = -1;
     for (int j = 0, t0 = 0; t0 < c; ++j, t0 += tm) {
@@ -155,19 +148,16 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
           o.items[2 * (ibase[e] + j) + 1] = t0;
         }
   }
-  __syncthreads();
-  for (int w = threadIdx.x; w < E * Q; w += 1024) {
-    const int e = w / Q, q = w - e * Q;
-    const int i0 = q * seg, i1 = min(n, i0 + seg);
-    int row = cnt[w];
-    for (int i = i0; i < i1; ++i) {
-      if (sid[i] == e) {
-        o.slot[i] = row;
-        if (row < o.max_rows) o.src[row] = i / topk;
-        if (o.lists) o.lists[(size_t)e * o.cap + (row - eoff[e])] = i;
-        ++row;
-      }
-    }
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) continue;
+    const int t = i / topk;
+    const unsigned long long word = bits[(size_t)e * W + (t >> 6)];
+    const int rank = pre[e * W + (t >> 6)] + __popcll(word & ((1ull << (t & 63)) - 1ull));
+    const int row = eoff[e] + rank;
+    o.slot[i] = row;
+    if (row < o.max_rows) o.src[row] = t;
+    if (o.lists && rank < o.cap) o.lists[(size_t)e * o.cap + rank] = i;
   }
   // rows past the last segment are never in a tile; mark them padding too
   for (int r = eoff[E] + threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;
@@ -195,70 +185,6 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
     }
     reinterpret_cast<float4*>(y + (size_t)t * d)[c] = acc;
   }
-}
-
-// ---- decode-time expert GEMVs (one token) ----
-// Lane share of W[row] . xs over K (x in LDS), 16-byte chunks c = lane, lane + 64, ...; G a multiple of 8.
-__device__ __forceinline__ float row_dot_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                                            size_t row, int K, int group, const float* xs, int lane) {
-  const int kw = K >> 3;
-  const int gpr = K / group;
-  float acc = 0.f;
-  for (int c = lane; c < (K >> 5); c += 64) {
-    const uint4 w4 = *reinterpret_cast<const uint4*>(wq + row * kw + c * 4);
-    const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float* xv = xs + c * 32 + j * 8;
-      const float xsum = ((xv[0] + xv[1]) + (xv[2] + xv[3])) + ((xv[4] + xv[5]) + (xv[6] + xv[7]));
-      const float sc = half_bits_to_float(ws[row * gpr + (c * 32 + j * 8) / group]);
-      acc = fmaf(dot8_biased(wv[j], xv) - 8.0f * xsum, sc, acc);
-    }
-  }
-  return acc;
-}
-
-// a[e, j] = silu(W[ids[e] * 2F + j] . x) * (W[ids[e] * 2F + F + j] . x): one wave per (e, j).
-__global__ __launch_bounds__(256) void k_moe_gate_up(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                                                     const int32_t* __restrict__ ids, const float* __restrict__ x,
-                                                     float* __restrict__ a, int F, int K, int group, int topk,
-                                                     int experts) {
-  extern __shared__ float xs[];
-  for (int i = threadIdx.x; i < K; i += 256) xs[i] = x[i];
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (o >= topk * F) return;
-  const int e = o / F, j = o - e * F;
-  const int ex = ids[e];
-  if (ex < 0 || ex >= experts) {  // an invalid id selects no weights
-    if (lane == 0) a[(size_t)e * F + j] = 0.f;
-    return;
-  }
-  const size_t row = (size_t)ex * 2 * F + j;
-  const float g = wave_sum(row_dot_q4(wq, ws, row, K, group, xs, lane));
-  const float u = wave_sum(row_dot_q4(wq, ws, row + F, K, group, xs, lane));
-  if (lane == 0) a[(size_t)e * F + j] = silu(g) * u;
-}
-
-// y[r] (+)= sum_e weights[e] * W[ids[e] * D + r] . a[e] (e in order): one wave per output row.
-__global__ __launch_bounds__(256) void k_moe_down(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                                                  const int32_t* __restrict__ ids, const float* __restrict__ weights,
-                                                  const float* __restrict__ a, float* __restrict__ y, int D, int F,
-                                                  int group, int topk, int add, int experts) {
-  extern __shared__ float as[];
-  for (int i = threadIdx.x; i < topk * F; i += 256) as[i] = a[i];
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= D) return;
-  float acc = 0.f;
-  for (int e = 0; e < topk; ++e) {
-    const int ex = ids[e];
-    if (ex < 0 || ex >= experts) continue;  // wave-uniform: an invalid id contributes nothing
-    acc = fmaf(weights[e], wave_sum(row_dot_q4(wq, ws, (size_t)ex * D + r, F, group, as + e * F, lane)), acc);
-  }
-  if (lane == 0) y[r] = add ? y[r] + acc : acc;
 }
 
 // ---- router: y[t, r] = W[r] . x[t] with fp32 W: one wave per (row, token) ----
@@ -313,9 +239,9 @@ extern "C" int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t 
   return (int32_t)((tokens * topk + (int64_t)experts * (tm - 1)) / tm);
 }
 
-static size_t group_lds(int64_t n, int E) {
-  const int Q = E >= 1024 ? 1 : 1024 / E;
-  return (size_t)(n + (int64_t)E * Q + 4 * (E + 1)) * 4;
+static size_t group_lds(int64_t tokens, int E) {
+  const int64_t W = (tokens + 63) / 64;
+  return (size_t)E * W * 12 + (size_t)4 * (E + 1) * 4;
 }
 
 extern "C" int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm,
@@ -327,7 +253,7 @@ extern "C" int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, in
       max_tiles < aq_moe_group_max_tiles(tokens, topk, experts, tm))
     return AQ_ERR_CAPACITY;
   const int64_t n = tokens * topk;
-  const size_t lds = group_lds(n, experts);
+  const size_t lds = group_lds(tokens, experts);
   if (lds > 160 * 1024) return AQ_ERR_CAPACITY;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k_moe_group), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -352,7 +278,7 @@ extern "C" int aq_moe_expert_lists(const int32_t* ids, int64_t tokens, int32_t t
   // the lists are the grouping with tm = 1 (no padding); its offsets, slots, src and tiles go to the scratch ints
   const int64_t need = (experts + 1) + n + n + 2 * n + 1;
   if (scratch_ints < need) return AQ_ERR_CAPACITY;
-  const size_t lds = group_lds(n, experts);
+  const size_t lds = group_lds(tokens, experts);
   if (lds > 160 * 1024) return AQ_ERR_CAPACITY;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k_moe_group), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -387,34 +313,6 @@ extern "C" int aq_moe_combine(const float* yd, int64_t yd_rows, const int32_t* s
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), yd,
                      slot, weights, y, (int)tokens, (int)d, topk, add, (int)yd_rows);
-  return launch_status();
-}
-
-extern "C" int aq_moe_gate_up_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids,
-                                 const float* x, float* a, int64_t f, int64_t k, int32_t group, int32_t topk,
-                                 void* stream) {
-  if (!wq || !ws || !ids || !x || !a) return AQ_ERR_NULL;
-  if (f <= 0 || k <= 0 || k % 32 || topk <= 0 || topk * f > (1 << 30) || experts <= 0) return AQ_ERR_SHAPE;
-  if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
-  if (k * 4 > 64 * 1024) return AQ_ERR_CAPACITY;
-  if (!aligned(wq, 16)) return AQ_ERR_ALIGN;
-  hipLaunchKernelGGL(k_moe_gate_up, dim3((unsigned)((topk * f + 3) / 4)), dim3(256), (size_t)k * 4,
-                     reinterpret_cast<hipStream_t>(stream), wq, ws, ids, x, a, (int)f, (int)k, group, topk,
-                     (int)experts);
-  return launch_status();
-}
-
-extern "C" int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t experts, const int32_t* ids,
-                              const float* weights, const float* a, float* y, int64_t d, int64_t f, int32_t group,
-                              int32_t topk, int32_t add, void* stream) {
-  if (!wq || !ws || !ids || !weights || !a || !y) return AQ_ERR_NULL;
-  if (d <= 0 || f <= 0 || f % 32 || topk <= 0 || d > (1 << 30) || experts <= 0) return AQ_ERR_SHAPE;
-  if (group <= 0 || group % 8 || f % group) return AQ_ERR_GROUP;
-  if (topk * f * 4 > 64 * 1024) return AQ_ERR_CAPACITY;
-  if (!aligned(wq, 16)) return AQ_ERR_ALIGN;
-  hipLaunchKernelGGL(k_moe_down, dim3((unsigned)((d + 3) / 4)), dim3(256), (size_t)topk * f * 4,
-                     reinterpret_cast<hipStream_t>(stream), wq, ws, ids, weights, a, y, (int)d, (int)f, group, topk,
-                     add, (int)experts);
   return launch_status();
 }
 

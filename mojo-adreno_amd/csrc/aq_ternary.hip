@@ -37,18 +37,15 @@ __device__ __forceinline__ float t2_word_dot(uint32_t w, const uint32_t* xp, flo
   return acc;
 }
 
-// Workgroup (column tile ct, split sp): columns [256 ct, +256) (lane l -> columns 4l..4l+3 of the tile, all four
-// waves), k-rows (16 k each) [sp * krows_wg, +krows_wg) divided among the four waves (whole 128-groups each).
-// MODE 0: fused GEMV, the last workgroup of a column tile to finish sums the split partials in split order.
-// MODE 1: reference partials (packed_linear): each workgroup covers 1024 k and writes partial[sp][n].
-template <int MODE, bool VEC4>
-__global__ __launch_bounds__(256) void k_t2_gemv(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
-                                                 const uint16_t* __restrict__ sc, float* __restrict__ y,
-                                                 float* __restrict__ part, int* __restrict__ counters, int N, int K,
-                                                 int krows_wg, int splits) {
+// The reference's split interface (packed_linear): workgroup (column tile ct, split sp) covers columns [256 ct, +256)
+// (lane l -> columns 4l..4l+3, all four waves) and k-rows [sp * krows_wg, +krows_wg) (1024 k), divided among the four
+// waves in whole 128-groups, and writes partial[sp][n].
+template <bool VEC4>
+__global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ sc, float* __restrict__ part, int N,
+                                                     int K, int krows_wg, int splits) {
   extern __shared__ uint32_t xs[];  // [krows_wg][8] scaled x pairs, then [4][256] floats for the wave reduction
   float* red = reinterpret_cast<float*>(xs + krows_wg * 8);
-  __shared__ int last;
   const int ct = blockIdx.x / splits;
   const int sp = blockIdx.x - ct * splits;
   const int kr0 = sp * krows_wg;
@@ -126,26 +123,81 @@ __global__ __launch_bounds__(256) void k_t2_gemv(const uint32_t* __restrict__ x2
   __syncthreads();
   const int n = ct * 256 + threadIdx.x;
   float v = ((red[threadIdx.x] + red[256 + threadIdx.x]) + red[512 + threadIdx.x]) + red[768 + threadIdx.x];
-  if (MODE == 1 || splits == 1) {
-    if (n < N) {
-      if (MODE == 1) part[(size_t)sp * N + n] = v;
-      else y[n] = v;
-    }
-    return;
-  }
   if (n < N) part[(size_t)sp * N + n] = v;
-  __threadfence();  // release: this workgroup's partials before its arrival is counted
-  __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(&counters[ct], 1) == splits - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // acquire: every other split's partials are visible
-  if (n < N) {
-    float acc = 0.f;
-    for (int s2 = 0; s2 < splits; ++s2) acc += __builtin_nontemporal_load(part + (size_t)s2 * N + n);
-    y[n] = acc;
+}
+
+// Fused ternary GEMV without any cross-workgroup step. A 512-thread workgroup owns CB consecutive columns over all
+// of K: lane l takes column l % CB and phase l / CB of its wave; the 8 * 64 / CB phases split the k-rows into
+// contiguous runs of whole 128-groups, so a load instruction reads CB consecutive words of 64/CB rows. Phase partials
+// are summed in phase order through LDS (deterministic). x' (scaled fp16 pairs) is staged in LDS once.
+template <int CB>
+__global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
+                                                      int K) {
+  constexpr int PH = 8 * 64 / CB;  // phases per workgroup
+  extern __shared__ uint32_t xs[];   // [K/16][8] scaled x pairs
+  __shared__ float red[PH][CB];
+  const int krows = K >> 4;
+  for (int i = threadIdx.x; i < krows * 8; i += 512) {
+    const int r = i >> 3, j = i & 7;
+    const int k = r * 16 + j;
+    const uint32_t lo = x2h[k >> 1], hi = x2h[(k + 8) >> 1];
+    const float a = half_bits_to_float((uint16_t)(k & 1 ? lo >> 16 : lo & 0xFFFF));
+    const float b = half_bits_to_float((uint16_t)((k + 8) & 1 ? hi >> 16 : hi & 0xFFFF));
+    const float f = t2_xscale(j);
+    xs[i] = (uint32_t)float_to_half_bits(a * f) | ((uint32_t)float_to_half_bits(b * f) << 16);
   }
-  if (threadIdx.x == 0) counters[ct] = 0;  // ready for the next call
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane % CB;
+  const int ph = wave * (64 / CB) + lane / CB;
+  const int n = blockIdx.x * CB + c;
+  const int groups = krows >> 3;  // 128-groups
+  const int g0 = (int)(((long)groups * ph) / PH), g1 = (int)(((long)groups * (ph + 1)) / PH);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(w), (short)0, (int)min((size_t)krows * N * 4, (size_t)0x7FFFFFFF), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(sc), (short)0,
+                                                                       (int)((size_t)groups * N * 2), 0x00020000);
+  uint32_t magic;  // the fp16-pair exponent bits in a VGPR, so each mask-and-OR is one v_and_or_b32
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  const bool col_ok = n < N;
+  float tot = 0.f;
+  for (int g = g0; g < g1; ++g) {
+    uint32_t wv[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      wv[r] = __builtin_amdgcn_raw_buffer_load_b32(wr, col_ok ? ((uint32_t)(g * 8 + r) * N + n) * 4 : 0x80000000u, 0,
+                                                   0);
+    const float s = half_bits_to_float(
+        __builtin_amdgcn_raw_buffer_load_b16(srs, col_ok ? ((uint32_t)g * N + n) * 2 : 0x80000000u, 0, 0));
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint4 x0 = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8);
+      const uint4 x1 = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8 + 4);
+      const uint32_t xp[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const uint32_t hi = wv[r] >> 10;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = j <= 4 ? j : j - 5;
+        const uint32_t bits = ((j <= 4 ? wv[r] : hi) & (0x00030003u << (2 * e))) | magic;
+        const _Float16 bias = (_Float16)(1024.0f + (float)(1 << (2 * e)));
+        const half2v h = __builtin_bit_cast(half2v, bits) - half2v{bias, bias};
+        if (j & 1) acc1 = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc1, false);
+        else acc0 = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc0, false);
+      }
+    }
+    tot = fmaf(acc0 + acc1, s, tot);
+  }
+  red[ph][c] = tot;
+  __syncthreads();
+  if (threadIdx.x < CB && blockIdx.x * CB + (int)threadIdx.x < N) {
+    float v = 0.f;
+#pragma unroll
+    for (int p = 0; p < PH; ++p) v += red[p][threadIdx.x];
+    y[blockIdx.x * CB + threadIdx.x] = v;
+  }
 }
 
 // y[n] = sum_g partials[g][n] in g order (bonsai/kernels/kernels.mojo:437-448, packed_reduce).
@@ -203,18 +255,18 @@ static int t2_check(const void* x2h, const void* w, const void* s, int64_t n, in
   return AQ_OK;
 }
 
-template <int MODE>
-static int launch_t2(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, float* part, int* counters,
-                     int N, int K, int krows_wg, int splits, hipStream_t st) {
+static int launch_t2_partials(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* part, int N, int K,
+                              hipStream_t st) {
+  const int krows_wg = 64;  // 1024 k
+  const int splits = (K + 1023) / 1024;
   const int ctiles = (N + 255) / 256;
   const size_t lds = (size_t)krows_wg * 8 * 4 + 4 * 256 * 4;
-  const bool vec4 = (N % 4) == 0;
-  if (vec4)
-    hipLaunchKernelGGL((k_t2_gemv<MODE, true>), dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, y, part,
-                       counters, N, K, krows_wg, splits);
+  if (N % 4 == 0)
+    hipLaunchKernelGGL(k_t2_partials<true>, dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, part, N, K, krows_wg,
+                       splits);
   else
-    hipLaunchKernelGGL((k_t2_gemv<MODE, false>), dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, y, part,
-                       counters, N, K, krows_wg, splits);
+    hipLaunchKernelGGL(k_t2_partials<false>, dim3(ctiles * splits), dim3(256), lds, st, x2h, w, s, part, N, K,
+                       krows_wg, splits);
   return launch_status();
 }
 
@@ -222,37 +274,29 @@ static int launch_t2(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, 
 
 using namespace aq;
 
-// Workspace layout, fixed for every shape so that counters never land on an earlier call's partials:
-// [0, 64 KiB) arrival counters (one int per 256-column tile, all zero between calls), then the fp32 partials.
-constexpr int64_t kT2CounterBytes = 64 * 1024;
-
 extern "C" int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k) {
-  if (n <= 0 || k <= 0) return 0;
-  const int64_t splits = (k + 511) / 512;
-  return splits > 1 ? kT2CounterBytes + splits * n * 4 : 0;
+  (void)n;
+  (void)k;
+  return 0;  // the fused kernel reduces inside each workgroup
 }
 
 extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int64_t n, int64_t k,
                           void* workspace, int64_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   int st = t2_check(x2h, w, s, n, k);
   if (st) return st;
   if (!y) return AQ_ERR_NULL;
+  const size_t lds = (size_t)(k / 16) * 8 * 4;  // x' staging: 8 scaled pairs per 16-k row = 2K bytes
+  if (lds > 64 * 1024) return AQ_ERR_CAPACITY;
   const int N = (int)n, K = (int)k;
-  int splits = (K + 511) / 512;
-  int krows_wg = 32;  // 512 k: one 128-group per wave
-  float* part = nullptr;
-  int* counters = nullptr;
-  if (splits > 1) {
-    const int64_t need = aq_t2_gemv_workspace_bytes(n, k);
-    if (!workspace || workspace_bytes < need || !aligned(workspace, 16) || (n + 255) / 256 > kT2CounterBytes / 4) {
-      splits = 1;  // no workspace: one workgroup per column tile covers all of K
-      krows_wg = K / 16;
-    } else {
-      counters = static_cast<int*>(workspace);
-      part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kT2CounterBytes);
-    }
-  }
-  return launch_t2<0>(x2h, w, s, y, part, counters, N, K, krows_wg, splits, reinterpret_cast<hipStream_t>(stream));
+  hipStream_t sm = reinterpret_cast<hipStream_t>(stream);
+  // 32-column blocks when that still gives >= 256 workgroups, else 16 (more workgroups, 64-byte segments)
+  if ((N + 31) / 32 >= 256)
+    hipLaunchKernelGGL(k_t2_gemv_cols<32>, dim3((unsigned)((N + 31) / 32)), dim3(512), lds, sm, x2h, w, s, y, N, K);
+  else
+    hipLaunchKernelGGL(k_t2_gemv_cols<16>, dim3((unsigned)((N + 15) / 16)), dim3(512), lds, sm, x2h, w, s, y, N, K);
+  return launch_status();
 }
 
 extern "C" int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials,
@@ -260,9 +304,7 @@ extern "C" int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const
   int st = t2_check(x2h, w, s, n, k);
   if (st) return st;
   if (!partials) return AQ_ERR_NULL;
-  const int splits = (int)((k + 1023) / 1024);
-  return launch_t2<1>(x2h, w, s, nullptr, partials, nullptr, (int)n, (int)k, 64, splits,
-                      reinterpret_cast<hipStream_t>(stream));
+  return launch_t2_partials(x2h, w, s, partials, (int)n, (int)k, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int aq_t2_packed_reduce(const float* partials, float* y, int64_t n, int32_t groups, void* stream) {
