@@ -1,0 +1,137 @@
+// Shared pieces of the MFMA GEMM kernels (aq_gemm.hip, aq_gemm_x16.hip): operand types, buffer-resource loads, the
+// kernel argument block, the tile decode and the epilogue.
+#pragma once
+#include "aq_common.h"
+
+namespace aq {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kSuper = 128;  // k per super-step
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+}
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zero (no branch needed).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource used here: the load returns zero
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return half_bits_to_float(h);
+}
+
+enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transposed words [K/16, N]
+
+// Kernel arguments (by value). Dense: X [M, K] -> y [M, N]. Grouped (MoE): work tile `it` of tiles[] is (expert e,
+// first grouped row m0); X row of grouped row g is src[g] (a token; -1 = padding, zeros) or g itself when src is
+// null; W rows of expert e start at e * n_per_expert; output rows are grouped rows (rows_total of them).
+struct GemmArgs {
+  const void* x;
+  const uint32_t* w;
+  const uint16_t* s;
+  float* y;
+  float* part;
+  uint16_t* act;           // SwiGLU epilogue output (fp16 bits) [rows_total, F]
+  const int* tiles;        // grouped: (expert, first row) pairs
+  const int* ntiles_dev;   // grouped: number of valid tiles (device)
+  const int* src;          // grouped: token of each grouped row, or null
+  int M, N, K, group, mtiles, ntiles, splits, sup_per_split;
+  int n_per_expert, F, rows_total;
+};
+
+enum { kDense = 0, kGrouped = 1, kGroupedSwiglu = 2 };
+
+// Work tile of this workgroup. Dense: ids are split into (xcd = id % 8, local = id / 8) when the grid is a multiple of
+// 8, so each XCD works through a contiguous run; within a run the m-tiles of one (n-tile, split) are adjacent (they
+// share W). Grouped: tile it of tiles[] = (expert, first grouped row). Returns false for workgroups with no tile.
+template <int MODE>
+__device__ __forceinline__ bool tile_of(const GemmArgs& ga, int BM, int& sp, int& nt, int& m0, int& expert) {
+  int id = blockIdx.x;
+  const int nblk = gridDim.x;
+  if constexpr (MODE == kDense) {
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int mt = id % ga.mtiles;
+    const int rest = id / ga.mtiles;
+    sp = rest % ga.splits;
+    nt = rest / ga.splits;
+    m0 = mt * BM;
+    return nt < ga.ntiles;
+  } else {
+    nt = id % ga.ntiles;
+    const int it = id / ga.ntiles;
+    if (it >= *ga.ntiles_dev) return false;
+    expert = ga.tiles[2 * it];
+    m0 = ga.tiles[2 * it + 1];
+    return true;
+  }
+}
+
+// Epilogue shared by the GEMM kernels: lane l holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows
+// and columns past the end.
+template <int MB, int NB, bool ADD, bool SPLIT, int MODE>
+__device__ __forceinline__ void gemm_store(const GemmArgs& ga, const float4v (&acc)[MB][NB], int m0, int nw0, int sp,
+                                           int lane) {
+  const int M = ga.M, N = ga.N;
+  float* __restrict__ y = ga.y;
+  float* __restrict__ part = ga.part;
+  const int bcol = lane & 15;
+  const int rq = (lane >> 4) * 4;
+  if constexpr (MODE == kGroupedSwiglu) {
+    const int F = ga.F;
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(ga.act, (uint32_t)((size_t)ga.rows_total * F * 2));
+#pragma unroll
+    for (int nb = 0; nb < NB / 2; ++nb) {
+      const int j = nw0 + nb * 16 + bcol;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int g = m0 + mb * 16 + rq + r;
+          const uint32_t off = j < F ? ((uint32_t)g * F + j) * 2 : kOOB;
+          const float v = silu(acc[mb][nb][r]) * acc[mb][nb + NB / 2][r];
+          __builtin_amdgcn_raw_buffer_store_b16(float_to_half_bits(v), a_rsrc, off, 0, 0);
+        }
+      }
+    }
+  } else {
+    const int rows_out = MODE == kDense ? M : ga.rows_total;
+    float* out = SPLIT ? part + (size_t)sp * M * N : y;
+    const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(out, (uint32_t)((size_t)rows_out * N * 4));
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n = nw0 + nb * 16 + bcol;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + mb * 16 + rq + r;
+          const uint32_t off = n < N ? ((uint32_t)m * N + n) * 4 : kOOB;
+          float v = acc[mb][nb][r];
+          if constexpr (ADD && !SPLIT)
+            v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// Launch the direct-to-LDS int4 GEMM (fp16 X, group a power of two >= 32) for MB row blocks, in aq_gemm_x16.hip.
+// Shapes it takes: K a multiple of 128 (whole super-steps) and a power-of-two group >= 32 (one scale per 32-k chunk).
+inline bool x16_shape_ok(int K, int group) {
+  return K > 0 && K % 128 == 0 && group >= 32 && (group & (group - 1)) == 0;
+}
+int launch_gemm_x16(const GemmArgs& ga, int mb, bool add, bool split, int mode, int blocks, hipStream_t s);
+
+}  // namespace aq

@@ -15,15 +15,9 @@
 // is staged once per workgroup in LDS in fragment order with the same k permutation (halves 0,4,1,5,2,6,3,7 of each
 // 8-chunk), so a fragment is one ds_read_b128 per lane; slots are XOR-swizzled to keep staging writes 2-way. LDS is
 // double-buffered: the next super-step's X and W are fetched into registers while this one is multiplied.
-#include "aq_common.h"
+#include "aq_gemm.h"
 
 namespace aq {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-
-constexpr int kSuper = 128;  // k per super-step
 
 // Swizzled LDS slot (16 bytes each) of the A fragment of (row-block mb, step s, lane l).
 __device__ __forceinline__ int a_slot(int mb, int s, int l) {
@@ -39,10 +33,6 @@ __device__ __forceinline__ uint4 permute8(uint4 d) {
   e.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
   e.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
   return e;
-}
-
-__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
-  return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
 }
 
 // One Q4W word -> MFMA B fragment (8 fp16 in the permuted k order) scaled by s2 = (scale, scale).
@@ -61,24 +51,6 @@ __device__ __forceinline__ half8 dequant_word(uint32_t w, half2v s2) {
   return out;
 }
 
-// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zero (no branch needed).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource used here: the load returns zero
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return __builtin_bit_cast(uint4, v);
-}
-
-__device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-  return half_bits_to_float(h);
-}
-
-enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transposed words [K/16, N]
-
 // One workgroup computes the BM x (4*NW) tile over super-steps [ks0, ks1). With SPLIT it writes its fp32 partial to
 // part[split][M][N]; otherwise to y (store or accumulate).
 //
@@ -86,25 +58,6 @@ enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transpose
 // step s takes word s/2, code positions j = 4(s%2) + t and j + 8 (t = 0..3) as fp16 pairs (1024 + c, via mask and
 // OR), minus 1025, times the column's fp16 scale for this 128-group. X is staged with the same pairing: 8-k chunks
 // A (k 0..7 of a 16-k word) and B (k 8..15) interleave as (A[4h+t], B[4h+t]).
-// Kernel arguments (by value). Dense: X [M, K] -> y [M, N]. Grouped (MoE): work tile `it` of tiles[] is (expert e,
-// first grouped row m0); X row of grouped row g is src[g] (a token; -1 = padding, zeros) or g itself when src is
-// null; W rows of expert e start at e * n_per_expert; output rows are grouped rows (rows_total of them).
-struct GemmArgs {
-  const void* x;
-  const uint32_t* w;
-  const uint16_t* s;
-  float* y;
-  float* part;
-  uint16_t* act;           // SwiGLU epilogue output (fp16 bits) [rows_total, F]
-  const int* tiles;        // grouped: (expert, first row) pairs
-  const int* ntiles_dev;   // grouped: number of valid tiles (device)
-  const int* src;          // grouped: token of each grouped row, or null
-  int M, N, K, group, mtiles, ntiles, splits, sup_per_split;
-  int n_per_expert, F, rows_total;
-};
-
-enum { kDense = 0, kGrouped = 1, kGroupedSwiglu = 2 };
-
 template <int FMT, int MB, int NB, bool G32, bool XF32, bool ADD, bool SPLIT, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
   const void* __restrict__ xv = ga.x;
@@ -122,26 +75,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
   constexpr int UL = (FMT == kT2 ? 2 : 1) * (XF32 ? 2 : 1);  // 16-byte loads per unit
   extern __shared__ uint4 lds[];                    // 2 stages x MB*4*64 fragment slots
 
-  // Tile order: ids are split into (xcd = id % 8, local = id / 8) when the grid is a multiple of 8, so each XCD
-  // works through a contiguous run; within a run the m-tiles of one (n-tile, split) are adjacent (they share W).
-  int id = blockIdx.x;
-  const int nblk = gridDim.x;
   int sp = 0, nt, m0, expert = 0;
-  if constexpr (MODE == kDense) {
-    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
-    const int mt = id % mtiles;
-    const int rest = id / mtiles;
-    sp = rest % splits;
-    nt = rest / splits;
-    if (nt >= ntiles) return;
-    m0 = mt * BM;
-  } else {
-    nt = id % ntiles;
-    const int it = id / ntiles;
-    if (it >= *ga.ntiles_dev) return;
-    expert = ga.tiles[2 * it];
-    m0 = ga.tiles[2 * it + 1];
-  }
+  if (!tile_of<MODE>(ga, BM, sp, nt, m0, expert)) return;
   const int nsup = (K + kSuper - 1) / kSuper;
   const int ks0 = sp * sup_per_split;
   const int ks1 = min(nsup, ks0 + sup_per_split);
@@ -339,46 +274,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows past the end ----
-  const int rq = (lane >> 4) * 4;
-  if constexpr (MODE == kGroupedSwiglu) {
-    const int F = ga.F;
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(ga.act, (uint32_t)((size_t)ga.rows_total * F * 2));
-#pragma unroll
-    for (int nb = 0; nb < NB / 2; ++nb) {
-      const int j = nw0 + nb * 16 + bcol;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int g = m0 + mb * 16 + rq + r;
-          const uint32_t off = j < F ? ((uint32_t)g * F + j) * 2 : kOOB;
-          const float v = silu(acc[mb][nb][r]) * acc[mb][nb + NB / 2][r];
-          __builtin_amdgcn_raw_buffer_store_b16(float_to_half_bits(v), a_rsrc, off, 0, 0);
-        }
-      }
-    }
-  } else {
-    const int rows_out = MODE == kDense ? M : ga.rows_total;
-    float* out = SPLIT ? part + (size_t)sp * M * N : y;
-    const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(out, (uint32_t)((size_t)rows_out * N * 4));
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int n = nw0 + nb * 16 + bcol;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + mb * 16 + rq + r;
-          const uint32_t off = n < N ? ((uint32_t)m * N + n) * 4 : kOOB;
-          float v = acc[mb][nb][r];
-          if constexpr (ADD && !SPLIT)
-            v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
-        }
-      }
-    }
-  }
+  gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
 }
 
 // y[i] = (add ? y[i] : 0) + sum_{s < splits} part[s][i], summed in split order (deterministic).
@@ -433,6 +329,15 @@ template <int FMT, int MB, bool G32, bool XF32, bool ADD, bool SPLIT>
 static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, float* y, float* part, int M, int N,
                        int K, int group, const GemmPlan& p, hipStream_t s) {
   constexpr int NB = 4;
+  int blocks = p.mtiles * p.ntiles * p.splits;
+  blocks = (blocks + 7) / 8 * 8;  // extra workgroups exit at once; a multiple of 8 enables the XCD mapping
+  GemmArgs ga{};
+  ga.x = x; ga.w = wq; ga.s = ws; ga.y = y; ga.part = part;
+  ga.M = M; ga.N = N; ga.K = K; ga.group = group; ga.mtiles = p.mtiles; ga.ntiles = p.ntiles;
+  ga.splits = p.splits; ga.sup_per_split = p.sup_per_split;
+  if constexpr (FMT == kQ4 && G32 && !XF32) {
+    if (x16_shape_ok(K, group)) return launch_gemm_x16(ga, MB, ADD, SPLIT, kDense, blocks, s);
+  }
   const size_t lds = 2 * (size_t)MB * 256 * 16;
   auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT, kDense>;
   if (lds > 64 * 1024) {
@@ -440,12 +345,6 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
                             (int)lds) != hipSuccess)
       return AQ_ERR_CAPACITY;
   }
-  int blocks = p.mtiles * p.ntiles * p.splits;
-  blocks = (blocks + 7) / 8 * 8;  // extra workgroups exit at once; a multiple of 8 enables the XCD mapping
-  GemmArgs ga{};
-  ga.x = x; ga.w = wq; ga.s = ws; ga.y = y; ga.part = part;
-  ga.M = M; ga.N = N; ga.K = K; ga.group = group; ga.mtiles = p.mtiles; ga.ntiles = p.ntiles;
-  ga.splits = p.splits; ga.sup_per_split = p.sup_per_split;
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();
 }
@@ -521,6 +420,9 @@ static int launch_grouped(const GemmArgs& ga0, int max_tiles, hipStream_t s) {
   ga.sup_per_split = (ga.K + kSuper - 1) / kSuper;
   const int blocks = ga.ntiles * max_tiles;
   if (blocks <= 0) return AQ_OK;
+  if constexpr (G32 && !XF32) {
+    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, MB, false, false, MODE, blocks, s);
+  }
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();
 }

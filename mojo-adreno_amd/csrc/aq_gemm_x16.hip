@@ -1,0 +1,244 @@
+// int4 (Q4W) prefill GEMM for fp16 X with one scale per 32-k chunk (group % 32 == 0) on CDNA4 matrix cores, gfx950:
+// the same product as aq_gemm.hip (llama/kernels/prefill/p_gemm_q4.mojo:106-142, lfm2/kernels/lk.mojo:458-495,
+// lfm2moe grouped p_gemm_q4g), with X staged by direct global-to-LDS loads. Built without the VGPR-form MFMA flag:
+// the accumulators live in AGPRs, which leaves the VGPRs to the operands.
+#include "aq_gemm.h"
+
+namespace aq {
+
+// ---- int4 GEMM for fp16 X, K % 128 == 0, group a power of two >= 32: direct-to-LDS staging ----------------------
+//
+// The MFMA k slots follow X's natural order: at step s of a super-step, lane l (row or column l%16, block b = l/16)
+// holds k = k0 + 32b + 8s + {0..7}. The A fragment of (row block mb, step s) is therefore 64 contiguous 16-byte pieces
+// of X, one per lane, and is fetched by one buffer_load_dwordx4 ... lds straight into fragment order (no registers,
+// no VALU, conflict-free ds_read_b128). Wave w fetches the fragments of step w for every row block. The B side is
+// the lane's word s of its 32-k chunk: byte t of the word holds k = 2t (low nibble) and 2t+1 (high nibble). One
+// v_perm_b32 copies byte t under the exponent bytes 0x64 (low half) and 0x54 (high half); masking the other nibble and
+// flipping bit 3 of the kept one (v_bitop3) gives the fp16 pair (1024 + q_lo, 64 + q_hi) with q = nib ^ 8, since the
+// mantissa LSB weighs 1 at 1024 and 1/16 at 64. Minus (1032, 72) this is the signed nibble exactly, times the scale.
+// Two named LDS buffers alternate, so the direct loads into one never alias the fragment reads of the other.
+__device__ __forceinline__ half8 dequant_q4_natural(uint32_t w, uint32_t s2bits) {
+  const uint32_t magic = 0x00005464u;  // bytes 4, 5 of the v_perm source pair: 0x64, 0x54
+  const half2v s2 = __builtin_bit_cast(half2v, s2bits);
+  const half2v bias = {(_Float16)1032.0f, (_Float16)72.0f};
+  half8 out;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t sel = 0x05000400u | ((uint32_t)t << 16) | (uint32_t)t;
+    const uint32_t x = (__builtin_amdgcn_perm(magic, w, sel) & 0xFFF0FF0Fu) ^ 0x00800008u;
+    const half2v h = (__builtin_bit_cast(half2v, x) - bias) * s2;
+    out[2 * t] = h[0];
+    out[2 * t + 1] = h[1];
+  }
+  return out;
+}
+
+// 16 bytes per lane from `r` at byte offset `off` into LDS at dst + 16 * lane (dst wave-uniform). A device-only
+// function: the address-space cast must not appear in host-visible code such as a lambda.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint4* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
+}
+
+template <int MB, int NB, bool ADD, bool SPLIT, int MODE>
+__global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
+  const uint32_t* __restrict__ wq = ga.w;
+  const uint16_t* __restrict__ ws = ga.s;
+  const int M = ga.M, N = ga.N, K = ga.K, group = ga.group;
+  constexpr int BM = 16 * MB;
+  constexpr int NW = 16 * NB;
+  constexpr int FR = MB * 4 * 64;  // uint4 slots per buffer: MB row blocks x 4 steps x 64 lanes
+  static_assert(NB == 4, "the W prefetch issues one column block per MFMA step");
+  __shared__ uint4 xa[FR];
+  __shared__ uint4 xb[FR];
+
+  int sp = 0, nt, m0, expert = 0;
+  if (!tile_of<MODE>(ga, BM, sp, nt, m0, expert)) return;
+  const int nsup = (K + kSuper - 1) / kSuper;
+  const int ks0 = sp * ga.sup_per_split;
+  const int ks1 = min(nsup, ks0 + ga.sup_per_split);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw0 = MODE == kGroupedSwiglu ? nt * (2 * NW) + wave * (NW / 2) : nt * (4 * NW) + wave * NW;
+  const int kw = K >> 3;
+  const int gpr = K / group;
+  const int gsh = 31 - __builtin_clz(group);  // group is a power of two >= 32 here
+
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(ga.x, (uint32_t)((size_t)M * K * 2));
+  const size_t wrows = MODE == kDense ? (size_t)N : (size_t)ga.n_per_expert * (size_t)ga.mtiles;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)(wrows * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)(wrows * gpr * 2));
+
+  // ---- staging. LDS block (mb, j) (1 KB) holds rows 16mb .. +15 of the tile over the j-th 32-k chunk of the
+  // super-step: row r's four 8-k pieces s sit in slots 4r + (s ^ sw(r)), sw(r) = (r >> 2) & 3, which makes the
+  // fragment reads below conflict-free. Wave w fetches chunk j = w of every row block; lane L takes row L/4 and slot
+  // L%4, so four consecutive lanes read one row's 64 contiguous bytes.
+  const int srow = lane >> 2;
+  const int spiece = (lane & 3) ^ ((srow >> 2) & 3);
+  uint32_t xoff[MB];  // byte offset of this lane's X row (kOOB past the end) plus its piece
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int g = m0 + mb * 16 + srow;
+    int m = g;
+    if constexpr (MODE != kDense) m = g < ga.rows_total ? (ga.src ? ga.src[g] : g) : -1;
+    xoff[mb] = ((m >= 0 && m < M) ? (uint32_t)m * (uint32_t)K * 2u : kOOB) + (uint32_t)spiece * 16u;
+  }
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto stage = [&](int ks, uint4* dst, int mb) {
+    const int k = ks * kSuper + 32 * wave_u;  // K % 128 == 0: always inside the row
+    lds_load16(x_rsrc, dst + (mb * 4 + wave_u) * 64, xoff[mb] + (uint32_t)k * 2u);
+  };
+  // fragment (mb, s) of this lane: block (mb, lane / 16), row lane % 16, piece s
+  const int arow = lane & 15;
+  const int aslot = (lane >> 4) * 64 + 4 * arow;
+  const int asw = (arow >> 2) & 3;
+
+  // ---- B source. Loads use a coalesced lane pattern: loader lane L = 4r + p fetches piece p (16 bytes: 32 k) of
+  // the super-step's 64 bytes of row r of a 16-column block, and its row's scale p & smask, so four consecutive lanes
+  // read contiguous memory. ds_bpermute then moves each word to the MFMA B layout (lane l = column l % 16, piece
+  // l / 16): the source of lane l is loader lane 4 (l % 16) + l / 16, and for its scale 4 (l % 16) + its group's index
+  // within the super-step.
+  const int lrow = lane >> 2;
+  const int lpiece = lane & 3;
+  const int smask = max((kSuper >> gsh) - 1, 0);  // scales per row and super-step, minus one (3, 1 or 0)
+  // Columns past the end read the last valid row instead (their sums are never stored), so the loads in the loop
+  // need no condition: a select there is turned into branches around the loads, with waits between them.
+  uint32_t wrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    int n;
+    if constexpr (MODE == kGroupedSwiglu) {
+      const int j = min(nw0 + (nb % (NB / 2)) * 16 + lrow, ga.F - 1);
+      n = nb < NB / 2 ? j : ga.F + j;
+    } else {
+      n = min(nw0 + nb * 16 + lrow, N - 1);
+    }
+    wrow[nb] = (uint32_t)expert * (uint32_t)ga.n_per_expert + (uint32_t)n;
+  }
+  const int waddr = 16 * (lane & 15) + 4 * (lane >> 4);
+  const int saddr = 16 * (lane & 15) + 4 * ((32 * (lane >> 4)) >> gsh);
+  // raw (loader-layout) W piece and scale bits of column block nb for super-step ks
+  auto load_b = [&](int ks, uint4 (&wr)[NB], uint32_t (&sr)[NB], int nb) {
+    const int k = ks * kSuper + 32 * lpiece;  // K % 128 == 0: always inside the row
+    wr[nb] = buf_load16(w_rsrc, wrow[nb] * (uint32_t)kw * 4u + (uint32_t)(k >> 3) * 4u);
+    const uint32_t g = (uint32_t)((ks * kSuper) >> gsh) + (uint32_t)(lpiece & smask);
+    sr[nb] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, (wrow[nb] * (uint32_t)gpr + g) * 2u, 0, 0);
+  };
+  auto bperm = [&](int addr, uint32_t v) -> uint32_t {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v);
+  };
+
+  struct WSet {
+    uint4 w[NB];
+    uint32_t s[NB];
+  };
+  float4v acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // Three W register sets rotate by name (the loop below is unrolled by 6 = lcm of 2 X buffers and 3 W sets), so no
+  // register that a load is still writing is ever copied: super-step ks multiplies one set while ks + 1's has landed
+  // and ks + 2's is in flight.
+  WSet w0, w1, w2;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) stage(ks0, xa, mb);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) load_b(ks0, w0.w, w0.s, nb);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) load_b(ks0 + 1 < ks1 ? ks0 + 1 : ks0, w1.w, w1.s, nb);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // One super-step: multiply the current slice from `cur` while fetching X of the next one into `nxt` (first, so the
+  // barrier can wait for it alone) and W of the one after (spread over the MFMA steps). The A fragments and B words
+  // of MFMA step s + 1 are read (LDS, ds_bpermute) during step s. Fetches past the end re-read the last slice: the X
+  // copy goes to the idle buffer, which nothing reads again.
+  auto step = [&](const uint4* cur, uint4* nxt, const WSet& cw, WSet& fw, int ks) {
+    const int kn = ks + 1 < ks1 ? ks + 1 : ks;
+    const int kf = ks + 2 < ks1 ? ks + 2 : ks;
+    const uint4(&wr)[NB] = cw.w;
+    const uint32_t(&sr)[NB] = cw.s;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) stage(kn, nxt, mb);
+    uint32_t s2[NB];
+    uint32_t bw[2][NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      s2[nb] = bperm(saddr, sr[nb]) * 0x00010001u;  // (scale, scale): the 16-bit load zero-extends
+      bw[0][nb] = bperm(waddr, wr[nb].x);
+    }
+    half8 a[2][MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) a[0][mb] = __builtin_bit_cast(half8, cur[mb * 256 + aslot + asw]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      load_b(kf, fw.w, fw.s, s);  // NB == 4: one column block per MFMA step
+      if (s < 3) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          a[(s + 1) & 1][mb] = __builtin_bit_cast(half8, cur[mb * 256 + aslot + ((s + 1) ^ asw)]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          bw[(s + 1) & 1][nb] = bperm(waddr, s == 0 ? wr[nb].y : s == 1 ? wr[nb].z : wr[nb].w);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const half8 b = dequant_q4_natural(bw[s & 1][nb], s2[nb]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s & 1][mb], b, acc[mb][nb], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Vector memory loads complete in issue order: with only this step's 2 * NB W and scale loads still allowed in
+    // flight, this wave's X loads into `nxt` (issued before them) have landed. vmcnt(8), expcnt/lgkmcnt unchanged.
+    static_assert(2 * NB == 8, "the wait below allows exactly the 2 * NB W and scale loads of fw in flight");
+    __builtin_amdgcn_s_waitcnt(0x0F78);
+    __syncthreads();  // ... and everyone's; `cur` may be overwritten from here on
+  };
+  for (int ks = ks0; ks < ks1; ks += 6) {
+    step(xa, xb, w0, w2, ks);
+    if (ks + 1 < ks1) step(xb, xa, w1, w0, ks + 1);
+    if (ks + 2 < ks1) step(xa, xb, w2, w1, ks + 2);
+    if (ks + 3 < ks1) step(xb, xa, w0, w2, ks + 3);
+    if (ks + 4 < ks1) step(xa, xb, w1, w0, ks + 4);
+    if (ks + 5 < ks1) step(xb, xa, w2, w1, ks + 5);
+  }
+  gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
+}
+
+template <int MB, int MODE>
+static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
+  constexpr int NB = 4;
+  if constexpr (MODE == kDense) {
+    if (split) hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, true, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    else if (add) hipLaunchKernelGGL((k_gemm_x16<MB, NB, true, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    else hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+  } else {
+    hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+  }
+}
+
+template <int MODE>
+static void launch_mode(const GemmArgs& ga, int mb, bool add, bool split, int blocks, hipStream_t s) {
+  switch (mb) {
+    case 1: return launch_mb<1, MODE>(ga, add, split, blocks, s);
+    case 2: return launch_mb<2, MODE>(ga, add, split, blocks, s);
+    case 3: return launch_mb<3, MODE>(ga, add, split, blocks, s);
+    case 4: return launch_mb<4, MODE>(ga, add, split, blocks, s);
+    case 5: return launch_mb<5, MODE>(ga, add, split, blocks, s);
+    case 6: return launch_mb<6, MODE>(ga, add, split, blocks, s);
+    default: return launch_mb<7, MODE>(ga, add, split, blocks, s);
+  }
+}
+
+// Grouped modes take neither `add` nor split-K. The caller has checked x16_shape_ok.
+int launch_gemm_x16(const GemmArgs& ga, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
+  if (mode == kDense) launch_mode<kDense>(ga, mb, add, split, blocks, s);
+  else if (mode == kGrouped) launch_mode<kGrouped>(ga, mb, false, false, blocks, s);
+  else launch_mode<kGroupedSwiglu>(ga, mb, false, false, blocks, s);
+  return launch_status();
+}
+
+}  // namespace aq

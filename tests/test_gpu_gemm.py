@@ -23,6 +23,10 @@ def _gemm(x, wq, ws, group, dev, add_to=None):
     (16, 64, 128, 32, False), (431, 256, 2048, 32, False), (144, 512, 256, 32, False), (37, 300, 160, 32, False),
     (1, 16, 32, 32, False), (431, 3072, 2048, 64, True), (288, 256, 512, 128, False), (64, 192, 256, 16, False),
     (50, 80, 96, 8, True), (500, 1024, 1024, 32, False),
+    # fp16 X with one, two or four scales per 128 k (one aligned scale load per row and super-step)
+    (431, 512, 2048, 64, False), (200, 768, 1024, 128, False), (64, 256, 2048, 256, False),
+    # scale rows that are not aligned for that load (K / group = 65, 33) take the general kernel
+    (100, 256, 2080, 32, False), (90, 128, 2112, 64, False),
 ])
 def test_kat_bit_exact(dev, m, n, k, group, xf32):
     """Integer-valued X, power-of-two scales: exact in fp16 and in fp32 accumulation, so the MFMA result must equal
