@@ -1,12 +1,16 @@
 """Benchmark of the weight-quantized matmul path on one MI355X; prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+    python bench.py --profile dominant|copy     # short runs for rocprofv3 --pmc passes
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
   value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
             (fused q|k|v 3072 x 2048, o 2048 x 2048, fused gate|up 16384 x 2048, down 2048 x 8192; G = 32), the
             layer's weights rotating over 16 distinct layers (547 MB, more than the 256 MB Infinity Cache). FLOPs
             count the true M (2 * 431 * 60.8 M weights = 52.4 GFLOP a step).
+  roofline  the dominant kernel, k_gemm_x16 on C1's gate|up (431 x 16384 x 2048, 28.9 GFLOP a launch), timed as a
+            graph burst of 48 launches with HIP events on its stream; traffic = HBM bytes a launch from the committed
+            rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/), scaled by a plain copy's counter reading.
   gemv_c0   C0 int4 decode GEMV (8192 x 2048, G = 32, fp32 x/y) GB/s over a rotating pool of >= 512 MB of distinct
             weight copies: graph burst (time per launch) and single cold launch.
 The K timed steps are replayed from hipGraphs.
@@ -168,6 +172,64 @@ def bench_gemm_c1(dev, steps: int, warmup: int, layers: int = 16):
                 weights_mb=round(layers * sum(n * k * 0.5625 for _, n, k in C1_LAYER) / 1e6, 1))
 
 
+DOMINANT = "k_gemm_x16<7, 4, false, false, 0>"  # the fused gate|up launch of C1 (16384 x 2048, M = 431)
+DOMINANT_SHAPE = (431, 16384, 2048)
+
+
+def _gate_up_launches(dev, layers: int = 16):
+    """The dominant kernel's launches: C1's gate|up GEMM over `layers` distinct weight copies."""
+    import torch
+    from aq import ops
+    m, n, k = DOMINANT_SHAPE
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(104)
+    x = torch.randn((m, k), device=dev, generator=gen).to(torch.float16)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    ws = [(torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=gen),
+           (torch.rand((n, k // 32), device=dev, generator=gen) * 0.03 + 1e-3).to(torch.float16))
+          for _ in range(layers)]
+    return [(lambda wq=wq, s_=s_: ops.gemm_q4(x, wq, s_, y, 32)) for wq, s_ in ws]
+
+
+def time_dominant(dev, rounds: int = 3):
+    """Average duration of one dominant-kernel launch: a hipGraph of `rounds` passes over the 16 weight copies,
+    replayed with HIP events recorded on the replay stream (the stream the kernels run on), divided by the launches.
+    The per-launch figure includes the graph's inter-kernel gap (about 1 us), so it sits slightly above the
+    kernel-trace average."""
+    launches = _gate_up_launches(dev) * rounds
+    t = GraphTimer(launches).time(replays=3) / len(launches)
+    m, n, k = DOMINANT_SHAPE
+    return dict(kernel=DOMINANT, flop=2 * m * n * k, t=t, launches=len(launches))
+
+
+def profile_run(dev, what: str):
+    """Short runs for rocprofv3 counter passes (see profiles/): the dominant kernel alone, or a plain copy of known
+    size that calibrates FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    if what == "dominant":
+        launches = _gate_up_launches(dev)
+        for fn in launches:
+            fn()
+    else:
+        nbytes = 256 << 20
+        a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": what, "done": True}), flush=True)
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes."""
+    f = ROOT / "profiles" / "k_gemm_x16_c1_gate_up_traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    return d.get("traffic_bytes") if d.get("kernel") == DOMINANT else None
+
+
 def _t2_gemv_bytes(n, k):
     return (k // 16) * n * 4 + (k // 128) * n * 2 + k * 2 + n * 4
 
@@ -282,6 +344,7 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--profile", choices=("dominant", "copy"), help="short run for a rocprofv3 counter pass")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
@@ -292,6 +355,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.profile:
+        profile_run(dev, args.profile)
+        return
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     c1 = bench_gemm_c1(dev, args.steps, args.warmup)
@@ -299,7 +365,9 @@ def main():
     r = bench_gemv_c0(dev, 128, 10)
     c2 = bench_ternary_c2(dev)
     c3 = bench_moe_c3(dev)
+    dom = time_dominant(dev)
     value = c1["flop"] / c1["t_step"] / 1e12
+    achieved = dom["flop"] / dom["t"] / 1e12
     gemv = r["bytes"] / r["t_burst"] / 1e9
     out = {
         "metric": "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms",
@@ -309,8 +377,10 @@ def main():
         "config": {"workload": "C1 int4 prefill GEMM: Llama-3.2-1B layer projections (q|k|v, o, gate|up, down) at "
                                "M=431, fp16 activations, G=32, weights rotating over 16 layers",
                    "tokens": 431, "weights_mb": c1["weights_mb"]},
-        "roofline": {"bound": "mfma", "achieved": round(value, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(value / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": load_traffic(),
+                     "kernel": dom["kernel"], "flop_per_launch": dom["flop"],
+                     "us_per_launch": round(dom["t"] * 1e6, 3)},
         "gemm_c1_per_projection": c1["per_gemm"],
         "gemv_c0": {"gbs_graph_burst": round(gemv, 2), "frac_hbm": round(gemv / HBM_PEAK_GBS, 4),
                     "gbs_single_cold": round(r["bytes"] / r["t_cold"] / 1e9, 2),
