@@ -21,9 +21,11 @@ Pinning status (how each function is checked, see tests/test_oracle_*.py):
     Python integer arithmetic, plus pure-Python brute force on tiny shapes.
   * route_top8: brute force (sort by (-logit, index)), forced ties, softmax->top-k->renormalise identity.
   * expert_lists/expert_items/p_group/combine: brute force with a stable sort (a library routine).
-  * quantize4 / quantize4_searched: bit-exact against the reference's own C (llama/st2bin.c, qwen3moe/convert.c)
-    compiled into oracle/_ref from the reference sources, where the reference tree is present.
-  * gguf_q4_0_to_q4w / gguf_q4_0_dequant: ggml's published Q4_0 block layout, re-derived independently in the test.
+  * quantize4 / quantize4_searched / gguf_q4_0_to_q4w / gguf_q4_0_dequant: bit-exact against the reference's own C
+    (llama/st2bin.c "q4", qwen3moe/convert.c "q4" for G = 32/64/128, lfm2/convert.c "q4" and "h4"), compiled from the
+    reference sources by oracle/Makefile: golden vectors in tests/golden/ref_*.npz (zero groups, .5 ties, fp16
+    subnormals, negative maxima) and, where oracle/_ref is built, fresh runs of the binaries
+    (tests/test_oracle_golden.py). Also ggml's published Q4_0 block layout, re-derived independently.
   * mlx_to_t2w: MLX's published 2-bit affine layout (weight = code*scale + bias), checked by dequantising both sides.
 The exact fp32 bits of the reference's Mojo kernels (its reduction order and MAX's warp/coop-matrix primitives)
 cannot be reproduced here: that part is "parity unpinned" and parity is defined by tolerance.
