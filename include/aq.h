@@ -169,6 +169,36 @@ int aq_rmsnorm_pack(const float* x, const float* w, uint32_t* q, int64_t rows, i
 /* q[row] = pack(silu(gate) * up), gu rows = gate (n) | up (n). Replaces: swiglu_pack (qwen3/kernels/qwen3k.mojo:51-59). */
 int aq_swiglu_pack(const float* gu, uint32_t* q, int64_t rows, int64_t n, void* stream);
 
+/* ---- weight-format converters (host code: host pointers, synchronous, no GPU) ----------------------------------
+ * They write the layouts above from the reference's source formats, byte for byte as the reference's converters do. */
+
+/* Q4W from fp16 weights (w_is_bf16 = 0) or from bf16 weights each rounded to fp16 first (w_is_bf16 = 1):
+ * s = fp16(max|w| / 7) per `group` weights of a row, q = clamp(rint(w / s), -8, 7) (0 where s == 0).
+ * w [rows, cols] -> wq [rows, cols/8], ws [rows, cols/group]. group % 8 == 0, cols % group == 0, group <= 4096.
+ * Replaces: quantize4 (llama/run.py:56-70) and the "q4" recipe line of llama/st2bin.c:44-66. */
+int aq_quantize_q4(const uint16_t* w, int32_t w_is_bf16, int64_t rows, int64_t cols, int32_t group, uint32_t* wq,
+                   uint16_t* ws);
+
+/* Q4W from bf16 weights with the least-squared-error scale fp16(m / d), d = 6.5, 6.75, ..., 9 (first minimum wins).
+ * group % 8 == 0, group <= 256. Replaces: the "q4" recipe line of qwen3moe/convert.c:120-159. */
+int aq_quantize_q4_searched(const uint16_t* w_bf16, int64_t rows, int64_t cols, int32_t group, uint32_t* wq,
+                            uint16_t* ws);
+
+/* GGUF Q4_0 (18-byte blocks of 32: fp16 d, then 16 bytes, element j low nibble of byte j, j + 16 its high nibble)
+ * -> Q4W words (nib ^ 8) and the fp16 scales unchanged (G = 32). cols % 32 == 0.
+ * Replaces: q4_block / the "q4" recipe line of lfm2/convert.c:59-71. */
+int aq_gguf_q4_0_to_q4w(const uint8_t* blocks, int64_t rows, int64_t cols, uint32_t* wq, uint16_t* ws);
+
+/* GGUF Q4_0 -> fp16 [rows, cols]: (nib - 8) * d in fp32, rounded to fp16.
+ * Replaces: q4_dequant + the "h4" recipe line of lfm2/convert.c:73-80. */
+int aq_gguf_q4_0_to_f16(const uint8_t* blocks, int64_t rows, int64_t cols, uint16_t* out);
+
+/* MLX 2-bit projections -> one fused T2W matrix: part p has codes [rows[p], K/16], scales and biases fp16
+ * [rows[p], K/128]; w [K/16, sum rows] (transposed), s [K/128, sum rows]. Returns AQ_ERR_ARG, writing nothing, if any
+ * group is not ternary (bias != -scale). K % 128 == 0. Replaces: addPacked (qwen3/convert.cpp:39-74). */
+int aq_t2w_from_mlx(const uint32_t* const* codes, const uint16_t* const* scales, const uint16_t* const* biases,
+                    const int64_t* rows, int32_t parts, int64_t k, uint32_t* w, uint16_t* s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,7 +42,7 @@ def _compile(src: Path) -> Path:
     if src.suffix == ".hip":
         cmd = [hipcc(), *DEVICE, *EXTRA.get(src.name, []), *COMMON, "-c", str(src), "-o", str(obj)]
     else:  # host-only C++ (format converters, status text): the system compiler, no device pass
-        cmd = ["g++", *COMMON, "-c", str(src), "-o", str(obj)]
+        cmd = ["g++", *COMMON, "-ffp-contract=off", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")
