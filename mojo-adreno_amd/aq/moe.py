@@ -2,7 +2,7 @@
 :253-266 for a prompt, and of lfm2moe/model.mojo:468-492's grouped prefill).
 
 Prompt (T tokens): route (top-k of the router logits) -> group (device histogram, padded prefix sum, stable
-permute, work tiles of ``tm`` rows) -> grouped gate|up GEMM with the SwiGLU product in its epilogue (fp16
+permute, work tiles of ``tm`` rows) -> fp32 tokens rounded to fp16 once -> grouped gate|up GEMM with the SwiGLU product in its epilogue (fp16
 activations) -> grouped down GEMM -> weighted combine in k order (+ residual). Decode (one token): route -> gate|up
 over the k chosen experts -> down summed over them. All buffers are allocated once, at construction, for at most
 ``max_tokens`` tokens; a forward call allocates nothing and never synchronises with the host.
@@ -19,7 +19,7 @@ class MoeBlock:
     ``[E * 2F, D/8]`` (expert e's gate rows at e*2F, up rows at e*2F + F) and down Q4W ``[E * D, F/8]``."""
 
     def __init__(self, gu_q, gu_s, dn_q, dn_s, experts: int, hidden: int, ffn: int, group: int, topk: int = 8,
-                 max_tokens: int = 512, tm: int = 32):
+                 max_tokens: int = 512, tm: int = 64):
         self.gu_q, self.gu_s, self.dn_q, self.dn_s = gu_q, gu_s, dn_q, dn_s
         self.E, self.D, self.F, self.G, self.K, self.tm = experts, hidden, ffn, group, topk, tm
         dev = gu_q.device
@@ -36,6 +36,7 @@ class MoeBlock:
         self.tiles = torch.empty(2 * self.max_tiles, **i32)
         self.ntiles = torch.empty(1, **i32)
         self.act = torch.empty((self.max_rows, ffn), dtype=torch.float16, device=dev)
+        self.xq = torch.empty((max_tokens, hidden // 2), **i32)  # fp32 tokens rounded to fp16 once (pairs)
         self.yd = torch.empty((self.max_rows, hidden), dtype=torch.float32, device=dev)
         self.a1 = torch.empty((topk, ffn), dtype=torch.float32, device=dev)
         self.none = torch.empty(0, **i32)
@@ -50,6 +51,9 @@ class MoeBlock:
         ops_.moe_route(logits, ids, wts, self.K)
         ops_.moe_group(ids, self.E, self.tm, self.counts, self.offs, self.slot[:t * self.K], self.src, self.tiles,
                        self.ntiles)
+        if x.dtype == torch.float32:  # one rounding to fp16 here, instead of one per expert tile in the GEMM
+            ops_.pack_half(x, self.xq[:t])
+            x = self.xq[:t].view(torch.float16)
         ops_.moe_gemm_q4(x, self.src, self.gu_q, self.gu_s, self.E, self.G, self.tiles, self.ntiles, self.tm, True,
                          self.act)
         ops_.moe_gemm_q4(self.act, self.none, self.dn_q, self.dn_s, self.E, self.G, self.tiles, self.ntiles, self.tm,

@@ -11,50 +11,58 @@
 namespace aq {
 
 // ---- routing: top-k of E logits per token, lowest index among equals; weights = softmax over the k winners ----
-// One wave per token. Each lane holds E/64 (<= 4) logits; k rounds of a (value, index) wave arg-max.
+// One wave per token. The wave's logits go to LDS; each lane ranks its E/64 (<= 4) logits against all E of them
+// (broadcast reads): rank = #{greater} + #{equal with a lower index}, so ranks are distinct and rank r < k is the
+// r-th winner. The weights are exp(v_r - v_0) / sum_{r < k} exp(v_r - v_0), summed in rank order.
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int32_t* __restrict__ ids,
                                                float* __restrict__ weights, int tokens, int E, int topk) {
+  __shared__ __align__(16) float lv[4][256];  // this wave's token's logits (E <= 256)
+  __shared__ float le[4][8];                  // exp(v_r - v_0) by rank
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= tokens) return;
+  const int w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
+  const bool active = t < tokens;  // no early return: every wave reaches the barriers
   float v[PER_LANE];
 #pragma unroll
   for (int j = 0; j < PER_LANE; ++j) {
     const int e = lane + 64 * j;
-    v[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
+    v[j] = (active && e < E) ? logits[(size_t)t * E + e] : -INFINITY;
+    lv[w][e] = v[j];  // slots >= E hold -inf and are never counted
   }
-  float top[8];
-  for (int k = 0; k < topk; ++k) {
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
+  __syncthreads();
+  int rank[PER_LANE];
 #pragma unroll
-    for (int j = 0; j < PER_LANE; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && (v[j] > best || (v[j] == best && e < bi))) {
-        best = v[j];
-        bi = e;
-      }
+  for (int j = 0; j < PER_LANE; ++j) rank[j] = 0;
+  float vmax = -INFINITY;
+  for (int e2 = 0; e2 < E; e2 += 4) {
+    const float4 x4 = *reinterpret_cast<const float4*>(&lv[w][e2]);
+    const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = e2 + q;
+      if (e >= E) break;
+      vmax = fmaxf(vmax, xs[q]);
+#pragma unroll
+      for (int j = 0; j < PER_LANE; ++j)
+        rank[j] += (xs[q] > v[j] || (xs[q] == v[j] && e < lane + 64 * j)) ? 1 : 0;
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ob = __shfl_xor(best, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      if (ob > best || (ob == best && oi < bi)) {
-        best = ob;
-        bi = oi;
-      }
-    }
-    top[k] = best;
-    if (lane == 0) ids[(size_t)t * topk + k] = bi;
-#pragma unroll
-    for (int j = 0; j < PER_LANE; ++j)
-      if (lane + 64 * j == bi) v[j] = -INFINITY;
   }
-  if (lane == 0) {
-    float total = 0.f;
-    for (int k = 0; k < topk; ++k) total += expf(top[k] - top[0]);
-    for (int k = 0; k < topk; ++k) weights[(size_t)t * topk + k] = expf(top[k] - top[0]) / total;
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    if (active && e < E && rank[j] < topk) {
+      ids[(size_t)t * topk + rank[j]] = e;
+      le[w][rank[j]] = expf(v[j] - vmax);
+    }
+  }
+  __syncthreads();
+  float total = 0.f;
+  for (int r = 0; r < topk; ++r) total += le[w][r];
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    if (active && e < E && rank[j] < topk) weights[(size_t)t * topk + rank[j]] = le[w][rank[j]] / total;
   }
 }
 
