@@ -34,18 +34,19 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
   int rank[PER_LANE];
 #pragma unroll
   for (int j = 0; j < PER_LANE; ++j) rank[j] = 0;
+  // Slots E .. 64 * PER_LANE - 1 hold -inf: they are greater than no logit, and tie only with the -inf of lanes that
+  // hold no expert, which write nothing. So the scan runs over whole float4s without a bound check.
   float vmax = -INFINITY;
-  for (int e2 = 0; e2 < E; e2 += 4) {
+  const int e_end = (E + 3) & ~3;
+  for (int e2 = 0; e2 < e_end; e2 += 4) {
     const float4 x4 = *reinterpret_cast<const float4*>(&lv[w][e2]);
     const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int e = e2 + q;
-      if (e >= E) break;
       vmax = fmaxf(vmax, xs[q]);
 #pragma unroll
       for (int j = 0; j < PER_LANE; ++j)
-        rank[j] += (xs[q] > v[j] || (xs[q] == v[j] && e < lane + 64 * j)) ? 1 : 0;
+        rank[j] += (int)((xs[q] > v[j]) | ((xs[q] == v[j]) & (e2 + q < lane + 64 * j)));  // branch-free
     }
   }
 #pragma unroll
@@ -94,81 +95,92 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
   const int T = n / topk;
   const int W = (T + 63) >> 6;
   int32_t* pre = reinterpret_cast<int32_t*>(bits + (size_t)E * W);  // [E][W] set bits before each word
-  int32_t* ecount = pre + E * W;     // [E]
-  int32_t* eoff = ecount + E;        // [E + 1]
-  int32_t* tbase = eoff + E + 1;     // [E + 1]
-  int32_t* ibase = tbase + E + 1;    // [E + 1]
+  int32_t* eoff = pre + E * W;   // [E + 1] first row of expert e's segment
+  int32_t* tbase = eoff + E + 1; // [E + 1] first work tile of expert e
+  int32_t* ibase = tbase + E + 1;// [E + 1] first work item of expert e (lists mode)
+  __shared__ int32_t wtot[16][3];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < E * W; i += 1024) bits[i] = 0ull;
+  for (int r = threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;  // padding rows; real rows are set below
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += 1024) {
     const int e = ids[i];
-    o.slot[i] = -1;  // stays -1 for an id outside [0, E): such an entry is in no group
-    if (e >= 0 && e < E) {
-      const int t = i / topk;
-      atomicOr(&bits[(size_t)e * W + (t >> 6)], 1ull << (t & 63));
-    }
+    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * W + ((i / topk) >> 6)], 1ull << ((i / topk) & 63));
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int run = 0;
+  // one thread per expert: count, padded rows, tiles, items; then exclusive scans over the experts (16 waves x 64)
+  int c = 0, rows = 0, nt = 0, ni = 0;
+  const int e = threadIdx.x;
+  if (e < E) {
     for (int w = 0; w < W; ++w) {
-      pre[e * W + w] = run;
-      run += __popcll(bits[(size_t)e * W + w]);
+      pre[e * W + w] = c;
+      c += __popcll(bits[(size_t)e * W + w]);
     }
-    ecount[e] = run;
+    nt = (c + tm - 1) / tm;
+    rows = nt * tm;
+    ni = o.items ? (c + o.items_tt - 1) / o.items_tt : 0;
+  }
+  int sr = rows, st = nt, si = ni;  // inclusive wave scans
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ur = __shfl_up(sr, d, 64), ut = __shfl_up(st, d, 64), ui = __shfl_up(si, d, 64);
+    if (lane >= d) {
+      sr += ur;
+      st += ut;
+      si += ui;
+    }
+  }
+  if (lane == 63) {
+    wtot[wave][0] = sr;
+    wtot[wave][1] = st;
+    wtot[wave][2] = si;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {  // prefix sums over experts
-    int off = 0, tb = 0, ib = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = ecount[e];
-      eoff[e] = off;
-      tbase[e] = tb;
-      ibase[e] = ib;
-      off += (c + tm - 1) / tm * tm;
-      tb += (c + tm - 1) / tm;
-      if (o.items) ib += (c + o.items_tt - 1) / o.items_tt;
-    }
-    eoff[E] = off;
-    tbase[E] = tb;
-    ibase[E] = ib;
-    o.ntiles[0] = tb;
-    if (o.nitems) o.nitems[0] = ib;
-    o.offs[E] = off;
+  int br = 0, bt = 0, bi = 0;
+  for (int v = 0; v < wave; ++v) {
+    br += wtot[v][0];
+    bt += wtot[v][1];
+    bi += wtot[v][2];
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    const int c = ecount[e];
+  if (e < E) {
+    eoff[e] = br + sr - rows;
+    tbase[e] = bt + st - nt;
+    ibase[e] = bi + si - ni;
     o.counts[e] = c;
     o.offs[e] = eoff[e];
-    const int pad_end = eoff[e] + (c + tm - 1) / tm * tm;
-    for (int r = eoff[e] + c; r < pad_end && r < o.max_rows; ++r) o.src[r] = -1;
-    for (int j = 0, t0 = 0; t0 < c; ++j, t0 += tm) {
+    for (int j = 0; j < nt; ++j)
       if (tbase[e] + j < o.max_tiles) {
         o.tiles[2 * (tbase[e] + j)] = e;
-        o.tiles[2 * (tbase[e] + j) + 1] = eoff[e] + t0;
+        o.tiles[2 * (tbase[e] + j) + 1] = eoff[e] + j * tm;
       }
-    }
     if (o.items)
-      for (int j = 0, t0 = 0; t0 < c; ++j, t0 += o.items_tt)
+      for (int j = 0; j < ni; ++j)
         if (ibase[e] + j < o.max_items) {
           o.items[2 * (ibase[e] + j)] = e;
-          o.items[2 * (ibase[e] + j) + 1] = t0;
+          o.items[2 * (ibase[e] + j) + 1] = j * o.items_tt;
         }
+    if (e == E - 1) {
+      o.offs[E] = br + sr;
+      o.ntiles[0] = bt + st;
+      if (o.nitems) o.nitems[0] = bi + si;
+    }
   }
+  __syncthreads();
   for (int i = threadIdx.x; i < n; i += 1024) {
-    const int e = ids[i];
-    if (e < 0 || e >= E) continue;
+    const int ex = ids[i];
+    if (ex < 0 || ex >= E) {
+      o.slot[i] = -1;  // an id outside [0, E) is in no group
+      continue;
+    }
     const int t = i / topk;
-    const unsigned long long word = bits[(size_t)e * W + (t >> 6)];
-    const int rank = pre[e * W + (t >> 6)] + __popcll(word & ((1ull << (t & 63)) - 1ull));
-    const int row = eoff[e] + rank;
+    const unsigned long long word = bits[(size_t)ex * W + (t >> 6)];
+    const int rank = pre[ex * W + (t >> 6)] + __popcll(word & ((1ull << (t & 63)) - 1ull));
+    const int row = eoff[ex] + rank;
     o.slot[i] = row;
     if (row < o.max_rows) o.src[row] = t;
-    if (o.lists && rank < o.cap) o.lists[(size_t)e * o.cap + rank] = i;
+    if (o.lists && rank < o.cap) o.lists[(size_t)ex * o.cap + rank] = i;
   }
-  // rows past the last segment are never in a tile; mark them padding too
-  for (int r = eoff[E] + threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;
 }
 
 // ---- combine: y[t, c] = (add ? y[t, c] : 0) + sum_k w[t, k] * yd[slot[t*topk + k], c], k in order ----
@@ -249,7 +261,7 @@ extern "C" int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t 
 
 static size_t group_lds(int64_t tokens, int E) {
   const int64_t W = (tokens + 63) / 64;
-  return (size_t)E * W * 12 + (size_t)4 * (E + 1) * 4;
+  return (size_t)E * W * 12 + (size_t)3 * (E + 1) * 4;
 }
 
 extern "C" int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm,

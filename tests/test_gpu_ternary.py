@@ -86,14 +86,17 @@ def test_packed_linear_and_reduce(dev, n, k):
     np.testing.assert_allclose(to_np(y), to_np(part).astype(np.float64).sum(0), rtol=1e-6, atol=1e-6)
 
 
-def test_pack_half_bit_exact(dev):
+@pytest.mark.parametrize("count,offset", [(4096, 0), (2006, 0), (2006, 2)])
+def test_pack_half_bit_exact(dev, count, offset):
+    """16-byte-aligned runs of 8 floats take the vector kernel, the ragged tail (2006 = 8 * 250 + 6) and a
+    misaligned x (offset 2 floats) the scalar one; both round to nearest even."""
     import torch
     rng = np.random.default_rng(1)
-    x = np.concatenate([rng.standard_normal(4094).astype(np.float32),
+    x = np.concatenate([rng.standard_normal(count + offset - 2).astype(np.float32),
                         np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11], np.float32)])  # ties to even
-    q = torch.empty(2048, dtype=torch.int32, device=dev)
-    _ops().pack_half(to_dev(x, dev), q)
-    np.testing.assert_array_equal(to_np(q).view(np.uint32), orc.x2h_pack(x))
+    q = torch.empty(count // 2, dtype=torch.int32, device=dev)
+    _ops().pack_half(to_dev(x, dev)[offset:], q)
+    np.testing.assert_array_equal(to_np(q).view(np.uint32), orc.x2h_pack(x[offset:]))
 
 
 def test_rmsnorm_and_swiglu_pack(dev):
