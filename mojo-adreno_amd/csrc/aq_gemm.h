@@ -127,11 +127,12 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& ga, const float4v (&a
   }
 }
 
-// Launch the direct-to-LDS int4 GEMM (fp16 X, group a power of two >= 32) for MB row blocks, in aq_gemm_x16.hip.
+// Launch the direct-to-LDS GEMM (fp16 X; Q4W with a power-of-two group >= 32, or T2W) for MB row blocks, in
+// aq_gemm_x16.hip.
 // Shapes it takes: K a multiple of 128 (whole super-steps) and a power-of-two group >= 32 (one scale per 32-k chunk).
 inline bool x16_shape_ok(int K, int group) {
   return K > 0 && K % 128 == 0 && group >= 32 && (group & (group - 1)) == 0;
 }
-int launch_gemm_x16(const GemmArgs& ga, int mb, bool add, bool split, int mode, int blocks, hipStream_t s);
+int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s);
 
 }  // namespace aq

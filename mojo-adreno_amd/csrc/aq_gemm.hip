@@ -336,8 +336,9 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
   ga.M = M; ga.N = N; ga.K = K; ga.group = group; ga.mtiles = p.mtiles; ga.ntiles = p.ntiles;
   ga.splits = p.splits; ga.sup_per_split = p.sup_per_split;
   if constexpr (FMT == kQ4 && G32 && !XF32) {
-    if (x16_shape_ok(K, group)) return launch_gemm_x16(ga, MB, ADD, SPLIT, kDense, blocks, s);
+    if (x16_shape_ok(K, group)) return launch_gemm_x16(ga, kQ4, MB, ADD, SPLIT, kDense, blocks, s);
   }
+  if constexpr (FMT == kT2 && !XF32) return launch_gemm_x16(ga, kT2, MB, ADD, SPLIT, kDense, blocks, s);
   const size_t lds = 2 * (size_t)MB * 256 * 16;
   auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT, kDense>;
   if (lds > 64 * 1024) {
@@ -421,7 +422,7 @@ static int launch_grouped(const GemmArgs& ga0, int max_tiles, hipStream_t s) {
   const int blocks = ga.ntiles * max_tiles;
   if (blocks <= 0) return AQ_OK;
   if constexpr (G32 && !XF32) {
-    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, MB, false, false, MODE, blocks, s);
+    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, kQ4, MB, false, false, MODE, blocks, s);
   }
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();

@@ -39,7 +39,32 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint4* dst,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
 }
 
-template <int MB, int NB, bool ADD, bool SPLIT, int MODE>
+// T2W (ternary) word w holds the 2-bit codes of 16 consecutive k of one column, code i at bits 2i; half h (k 8h .. 8h + 7)
+// is one MFMA step's B operand. Pair t = (code 2t, 2t + 1) sits in byte 2h + t/2 at bits 4(t % 2) and 4(t % 2) + 2.
+// v_perm copies that byte under two exponent bytes whose mantissa LSB makes the code's bits weigh 1: 0x64 (1024) and
+// 0x5C (256) for bits 0 and 2, 0x54 (64) and 0x4C (16) for bits 4 and 6; masking the other codes gives (1024 + c,
+// 256 + c') or (64 + c, 16 + c'), minus (1025, 257) / (65, 17) is (c - 1, c' - 1) exactly, times the scale.
+__device__ __forceinline__ half8 dequant_t2_natural(uint32_t w, int h, uint32_t s2bits) {
+  const uint32_t magic = 0x4C545C64u;  // bytes 4..7 of the v_perm source pair: 0x64, 0x5C, 0x54, 0x4C
+  const half2v s2 = __builtin_bit_cast(half2v, s2bits);
+  half8 out;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t b = (uint32_t)(2 * h + (t >> 1));
+    const uint32_t sel = ((t & 1) ? 0x07000600u : 0x05000400u) | (b << 16) | b;
+    const uint32_t mask = (t & 1) ? 0xFFC0FF30u : 0xFF0CFF03u;
+    const half2v bias = (t & 1) ? half2v{(_Float16)65.0f, (_Float16)17.0f} : half2v{(_Float16)1025.0f, (_Float16)257.0f};
+    const uint32_t x = __builtin_amdgcn_perm(magic, w, sel) & mask;
+    const half2v v = (__builtin_bit_cast(half2v, x) - bias) * s2;
+    out[2 * t] = v[0];
+    out[2 * t + 1] = v[1];
+  }
+  return out;
+}
+
+// FMT kQ4: Q4W rows [N, K/8] with fp16 scales [N, K/group]; kT2: T2W words [K/16, N] with scales [K/128, N] (dense
+// mode only). T2W is column-contiguous, so its loads are coalesced in the MFMA B layout directly (no ds_bpermute).
+template <int FMT, int MB, int NB, bool ADD, bool SPLIT, int MODE>
 __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
   const uint32_t* __restrict__ wq = ga.w;
   const uint16_t* __restrict__ ws = ga.s;
@@ -61,12 +86,14 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
   const int nw0 = MODE == kGroupedSwiglu ? nt * (2 * NW) + wave * (NW / 2) : nt * (4 * NW) + wave * NW;
   const int kw = K >> 3;
   const int gpr = K / group;
-  const int gsh = 31 - __builtin_clz(group);  // group is a power of two >= 32 here
+  const int gsh = 31 - __builtin_clz(group);  // group is a power of two >= 32 here (128 for T2W)
 
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(ga.x, (uint32_t)((size_t)M * K * 2));
   const size_t wrows = MODE == kDense ? (size_t)N : (size_t)ga.n_per_expert * (size_t)ga.mtiles;
-  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)(wrows * kw * 4));
-  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)(wrows * gpr * 2));
+  const __amdgpu_buffer_rsrc_t w_rsrc =
+      make_rsrc(wq, (uint32_t)(FMT == kT2 ? (size_t)(K >> 4) * N * 4 : wrows * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc =
+      make_rsrc(ws, (uint32_t)(FMT == kT2 ? (size_t)(K >> 7) * N * 2 : wrows * gpr * 2));
 
   // ---- staging. LDS block (mb, j) (1 KB) holds rows 16mb .. +15 of the tile over the j-th 32-k chunk of the
   // super-step: row r's four 8-k pieces s sit in slots 4r + (s ^ sw(r)), sw(r) = (r >> 2) & 3, which makes the
@@ -110,21 +137,29 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
       const int j = min(nw0 + (nb % (NB / 2)) * 16 + lrow, ga.F - 1);
       n = nb < NB / 2 ? j : ga.F + j;
     } else {
-      n = min(nw0 + nb * 16 + lrow, N - 1);
+      n = min(nw0 + nb * 16 + (FMT == kT2 ? (lane & 15) : lrow), N - 1);
     }
-    wrow[nb] = (uint32_t)expert * (uint32_t)ga.n_per_expert + (uint32_t)n;
+    wrow[nb] = (uint32_t)expert * (uint32_t)ga.n_per_expert + (uint32_t)n;  // T2W: the column
   }
   const int waddr = 16 * (lane & 15) + 4 * (lane >> 4);
   const int saddr = 16 * (lane & 15) + 4 * ((32 * (lane >> 4)) >> gsh);
   // raw (loader-layout) W piece and scale bits of column block nb for super-step ks
   auto load_b = [&](int ks, uint4 (&wr)[NB], uint32_t (&sr)[NB], int nb) {
-    const int k = ks * kSuper + 32 * lpiece;  // K % 128 == 0: always inside the row
-    wr[nb] = buf_load16(w_rsrc, wrow[nb] * (uint32_t)kw * 4u + (uint32_t)(k >> 3) * 4u);
-    const uint32_t g = (uint32_t)((ks * kSuper) >> gsh) + (uint32_t)(lpiece & smask);
-    sr[nb] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, (wrow[nb] * (uint32_t)gpr + g) * 2u, 0, 0);
+    if constexpr (FMT == kT2) {  // the two words (32 k) of block l / 16 and the column's scale, B layout as loaded
+      const uint32_t r = (uint32_t)(ks * (kSuper / 16) + 2 * (lane >> 4));
+      wr[nb].x = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, (r * (uint32_t)N + wrow[nb]) * 4u, 0, 0);
+      wr[nb].y = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc, ((r + 1) * (uint32_t)N + wrow[nb]) * 4u, 0, 0);
+      sr[nb] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, ((uint32_t)ks * (uint32_t)N + wrow[nb]) * 2u, 0, 0);
+    } else {
+      const int k = ks * kSuper + 32 * lpiece;  // K % 128 == 0: always inside the row
+      wr[nb] = buf_load16(w_rsrc, wrow[nb] * (uint32_t)kw * 4u + (uint32_t)(k >> 3) * 4u);
+      const uint32_t g = (uint32_t)((ks * kSuper) >> gsh) + (uint32_t)(lpiece & smask);
+      sr[nb] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, (wrow[nb] * (uint32_t)gpr + g) * 2u, 0, 0);
+    }
   };
-  auto bperm = [&](int addr, uint32_t v) -> uint32_t {
-    return (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v);
+  auto bperm = [&](int addr, uint32_t v) -> uint32_t {  // T2W arrives in the B layout already
+    if constexpr (FMT == kT2) return v;
+    else return (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v);
   };
 
   struct WSet {
@@ -180,11 +215,13 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
           a[(s + 1) & 1][mb] = __builtin_bit_cast(half8, cur[mb * 256 + aslot + ((s + 1) ^ asw)]);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          bw[(s + 1) & 1][nb] = bperm(waddr, s == 0 ? wr[nb].y : s == 1 ? wr[nb].z : wr[nb].w);
+          bw[(s + 1) & 1][nb] = FMT == kT2 ? (s + 1 < 2 ? wr[nb].x : wr[nb].y)
+                                           : bperm(waddr, s == 0 ? wr[nb].y : s == 1 ? wr[nb].z : wr[nb].w);
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const half8 b = dequant_q4_natural(bw[s & 1][nb], s2[nb]);
+        const half8 b = FMT == kT2 ? dequant_t2_natural(bw[s & 1][nb], s & 1, s2[nb])
+                                   : dequant_q4_natural(bw[s & 1][nb], s2[nb]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s & 1][mb], b, acc[mb][nb], 0, 0, 0);
@@ -208,36 +245,37 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
   gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
 }
 
-template <int MB, int MODE>
+template <int FMT, int MB, int MODE>
 static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
   constexpr int NB = 4;
   if constexpr (MODE == kDense) {
-    if (split) hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, true, MODE>), dim3(blocks), dim3(256), 0, s, ga);
-    else if (add) hipLaunchKernelGGL((k_gemm_x16<MB, NB, true, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
-    else hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    else hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
   } else {
-    hipLaunchKernelGGL((k_gemm_x16<MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
   }
 }
 
-template <int MODE>
+template <int FMT, int MODE>
 static void launch_mode(const GemmArgs& ga, int mb, bool add, bool split, int blocks, hipStream_t s) {
   switch (mb) {
-    case 1: return launch_mb<1, MODE>(ga, add, split, blocks, s);
-    case 2: return launch_mb<2, MODE>(ga, add, split, blocks, s);
-    case 3: return launch_mb<3, MODE>(ga, add, split, blocks, s);
-    case 4: return launch_mb<4, MODE>(ga, add, split, blocks, s);
-    case 5: return launch_mb<5, MODE>(ga, add, split, blocks, s);
-    case 6: return launch_mb<6, MODE>(ga, add, split, blocks, s);
-    default: return launch_mb<7, MODE>(ga, add, split, blocks, s);
+    case 1: return launch_mb<FMT, 1, MODE>(ga, add, split, blocks, s);
+    case 2: return launch_mb<FMT, 2, MODE>(ga, add, split, blocks, s);
+    case 3: return launch_mb<FMT, 3, MODE>(ga, add, split, blocks, s);
+    case 4: return launch_mb<FMT, 4, MODE>(ga, add, split, blocks, s);
+    case 5: return launch_mb<FMT, 5, MODE>(ga, add, split, blocks, s);
+    case 6: return launch_mb<FMT, 6, MODE>(ga, add, split, blocks, s);
+    default: return launch_mb<FMT, 7, MODE>(ga, add, split, blocks, s);
   }
 }
 
-// Grouped modes take neither `add` nor split-K. The caller has checked x16_shape_ok.
-int launch_gemm_x16(const GemmArgs& ga, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
-  if (mode == kDense) launch_mode<kDense>(ga, mb, add, split, blocks, s);
-  else if (mode == kGrouped) launch_mode<kGrouped>(ga, mb, false, false, blocks, s);
-  else launch_mode<kGroupedSwiglu>(ga, mb, false, false, blocks, s);
+// Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok.
+int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
+  if (fmt == kT2) launch_mode<kT2, kDense>(ga, mb, add, split, blocks, s);
+  else if (mode == kDense) launch_mode<kQ4, kDense>(ga, mb, add, split, blocks, s);
+  else if (mode == kGrouped) launch_mode<kQ4, kGrouped>(ga, mb, false, false, blocks, s);
+  else launch_mode<kQ4, kGroupedSwiglu>(ga, mb, false, false, blocks, s);
   return launch_status();
 }
 
