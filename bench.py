@@ -13,6 +13,8 @@ Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEM
             rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/), scaled by a plain copy's counter reading.
   gemv_c0   C0 int4 decode GEMV (8192 x 2048, G = 32, fp32 x/y) GB/s over a rotating pool of >= 512 MB of distinct
             weight copies: graph burst (time per launch) and single cold launch.
+  decode_c4 C4 Llama-3.2-1B decode step at context 512 (int4 linears incl. lm_head, fp16 KV cache): tokens/s of
+            graph-replayed steps, and GB/s over the 711.9 MB a step must read.
 The K timed steps are replayed from hipGraphs.
 Inputs are synthetic (seeded), resident in HBM before the timed region. ``--gpus N`` with N > 1 exits: this build
 measures one GPU.
@@ -311,6 +313,52 @@ def bench_moe_c3(dev):
                 gbs_1_active=round(8 * (1536 * 2048 + 2048 * 768) * 0.5625 / t1 / 1e9, 1))
 
 
+def bench_decode_c4(dev, replays: int = 40):
+    """C4: a full Llama-3.2-1B-architecture decode step (random int4 weights drawn on the device, 695 MB of linears,
+    fp16 embedding table) at context 512: the KV cache holds random fp16 rows 0..510 and the step at position 511
+    appends row 511 and attends over all 512. One step = 83 launches replayed from one hipGraph (the token each step
+    feeds back is the previous step's device argmax; the position stays at 511)."""
+    import torch
+    from aq.llama import LlamaConfig, LlamaDecoder, LlamaWeights
+    cfg = LlamaConfig()
+    dec = LlamaDecoder(LlamaWeights.random(cfg, 4, dev))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(104)
+    for kc, vc in zip(dec.kc, dec.vc):
+        kc.normal_(generator=gen)
+        vc.normal_(generator=gen)
+    dec.token.fill_(128000)
+    dec.pos.fill_(cfg.max_pos - 1)
+    t = GraphTimer([lambda: dec.step(advance=0)]).time(replays=replays)
+    nbytes = cfg.weight_bytes() + cfg.kv_bytes(cfg.max_pos)
+    out = dict(tok_s=round(1 / t, 1), us_per_token=round(t * 1e6, 2), bytes_per_token=nbytes,
+               gbs=round(nbytes / t / 1e9, 1), frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), context=512,
+               launches_per_step=1 + 5 * cfg.layers + 2)
+    del dec
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline_decode():
+    import numpy as np
+    from aq import synth
+    from aq.llama import LlamaConfig
+    from oracle import cpu_baseline as cb
+    cores = cb.threads()
+    cfg, sample = LlamaConfig(), 2
+    rng = np.random.default_rng(4)
+    d, f = cfg.dim, cfg.ffn
+    mats = [{name: synth.int4_matrix(rng, n, k, 32) for name, n, k in
+             (("wqkv", cfg.qkv, d), ("wo", d, d), ("wgu", 2 * f, d), ("wdown", d, f))} for _ in range(sample)]
+    t_layers, t_head = cb.llama_decode(mats, synth.int4_matrix(rng, cfg.vocab, d, 32), d, cfg.heads, cfg.kv_heads, f,
+                                       cfg.max_pos, 32)
+    per_token = t_head + t_layers * cfg.layers / sample
+    return dict(value=round(1 / per_token, 2), unit="tokens/s", cores=cores, kind="port",
+                sample=f"C4 decode at context 512: {sample} of 16 layers + lm_head/argmax timed (torch fp32 over "
+                       f"dequantised weights, fp32 cache, median of <=5 reps on {cb.cpu_model()}), "
+                       f"per token = head + 8 x the 2 layers")
+
+
 def cpu_baseline_gemm():
     import numpy as np
     from aq import synth
@@ -365,6 +413,7 @@ def main():
     r = bench_gemv_c0(dev, 128, 10)
     c2 = bench_ternary_c2(dev)
     c3 = bench_moe_c3(dev)
+    c4 = bench_decode_c4(dev)
     dom = time_dominant(dev)
     value = c1["flop"] / c1["t_step"] / 1e12
     achieved = dom["flop"] / dom["t"] / 1e12
@@ -388,11 +437,13 @@ def main():
                     "pool_mb": r["pool_mb"]},
         "ternary_c2": c2,
         "moe_c3": c3,
+        "decode_c4": c4,
         "wall_s": round(wall, 2),
     }
     if not args.skip_cpu:
         out["cpu_baseline"] = cpu_baseline_gemm()
         out["gemv_c0"]["cpu_baseline"] = cpu_baseline_gemv()
+        out["decode_c4"]["cpu_baseline"] = cpu_baseline_decode()
     print(json.dumps(out), flush=True)
 
 

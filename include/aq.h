@@ -169,6 +169,49 @@ int aq_rmsnorm_pack(const float* x, const float* w, uint32_t* q, int64_t rows, i
 /* q[row] = pack(silu(gate) * up), gu rows = gate (n) | up (n). Replaces: swiglu_pack (qwen3/kernels/qwen3k.mojo:51-59). */
 int aq_swiglu_pack(const float* gu, uint32_t* q, int64_t rows, int64_t n, void* stream);
 
+/* ---- Llama decode step (one token): the kernels around the int4 GEMVs -------------------------------------------
+ * The reference's step (llama/model.mojo:128-166) launches embed, then per layer rmsnorm, gemv_q4 (qkv), rope_kv,
+ * attention, gemv_add_q4 (o), rmsnorm, gemv_q4 (gate|up), silu_mul, gemv_add_q4 (down), then rmsnorm and the lm_head;
+ * the host then scans the logits for the argmax (llama/llama.mojo:72-75). Here the norms and silu_mul are fused into
+ * the GEMVs that consume them, RoPE and the cache append into attention, and the argmax runs on the device, so a step
+ * is 1 + 5 per layer + 2 launches. Token and position live in device memory (int32), so a captured step replays
+ * without host work. */
+
+/* y = W . rmsnorm(x), rmsnorm(x) = x * (1 / sqrt(mean(x^2) + eps)) * norm_w (fp16 [K]), per token; as aq_gemv_q4
+ * otherwise (add = 0). Replaces: rmsnorm (llama/kernels/rmsnorm.mojo:17-35) + gemv_q4 (gemv_q4.mojo:13-30), the pair
+ * at llama/model.mojo:146-147. norm_w 16-byte aligned. */
+int aq_rmsnorm_gemv_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w, float eps,
+                       float* y, int64_t n, int64_t k, int32_t group, int32_t tokens, void* stream);
+
+/* a = silu(W_gate . rmsnorm(x)) * (W_up . rmsnorm(x)), W = gate|up [2f, K]. Replaces: rmsnorm + gemv_q4 (wgu) +
+ * silu_mul (llama/kernels/silu_mul.mojo:9-12), llama/model.mojo:151-153. */
+int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w, float eps,
+                          float* a, int64_t f, int64_t k, int32_t group, int32_t tokens, void* stream);
+
+/* x[i] = table[*token, i] as fp32, table fp16 [vocab, d], d % 8 == 0 (a token outside [0, vocab) reads row 0).
+ * Replaces: embed (llama/kernels/embed.mojo:9-11; llama/model.mojo:142-143, which picks one of 4 table chunks). */
+int aq_embed_f16(const uint16_t* table, int64_t vocab, int64_t d, const int32_t* token, float* x, void* stream);
+
+/* Attention of the token at position p = *pos: RoPE (rotate_half, cos/sin fp32 [max_pos, head_dim/2]) on q and k of
+ * qkv fp32 [(heads + 2 kv_heads) * head_dim]; k and v stored at row p of k_cache/v_cache fp16 [kv_heads, max_pos,
+ * head_dim]; out[h] = softmax_s(q_h . k_s / sqrt(head_dim)) . v_s over s <= p, fp32 [heads * head_dim]. head_dim = 64,
+ * heads / kv_heads in {1, 2, 4, 8}, LDS (heads / kv_heads) * (max_pos + 2120) floats <= 160 KB (max_pos <= 8120 for
+ * 4 query heads per KV head). A p outside [0, max_pos) writes zeros
+ * and leaves the cache alone. Replaces: rope_kv (llama/kernels/rope_kv.mojo:18-45) + attention (attention.mojo:19-66),
+ * llama/model.mojo:148-150; the reference caches fp32. */
+int aq_attn_decode(const float* qkv, const float* cos_tab, const float* sin_tab, uint16_t* k_cache, uint16_t* v_cache,
+                   const int32_t* pos, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_pos, float* out,
+                   void* stream);
+
+/* Final norm, lm_head and greedy argmax: logits = W . rmsnorm(x) (norm_w NULL: x as given), then *token = the first
+ * index of the largest logit, hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance.
+ * cand: device scratch of AQ_HEAD_CANDIDATES argmax keys (8-byte aligned). Replaces: Llama.head
+ * (llama/model.mojo:160-166) and the host argmax scan (llama/llama.mojo:72-75). */
+#define AQ_HEAD_CANDIDATES 4096
+int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w, float eps,
+                      float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand, int64_t cand_cap,
+                      int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap, int32_t advance, void* stream);
+
 /* ---- weight-format converters (host code: host pointers, synchronous, no GPU) ----------------------------------
  * They write the layouts above from the reference's source formats, byte for byte as the reference's converters do. */
 

@@ -42,6 +42,12 @@ SIGNATURES: dict[str, list] = {
     "aq_pack_half": [_p, _p, _i64, _p],
     "aq_rmsnorm_pack": [_p, _p, _p, _i64, _i64, ctypes.c_float, _p],
     "aq_swiglu_pack": [_p, _p, _i64, _i64, _p],
+    "aq_rmsnorm_gemv_q4": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _i32, _i32, _p],
+    "aq_rmsnorm_gate_up_q4": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _i32, _i32, _p],
+    "aq_embed_f16": [_p, _i64, _i64, _p, _p, _p],
+    "aq_attn_decode": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _p, _p],
+    "aq_head_argmax_q4": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _i32, _i32,
+                          _p],
     "aq_quantize_q4": [_p, _i32, _i64, _i64, _i32, _p, _p],
     "aq_quantize_q4_searched": [_p, _i64, _i64, _i32, _p, _p],
     "aq_gguf_q4_0_to_q4w": [_p, _i64, _i64, _p, _p],

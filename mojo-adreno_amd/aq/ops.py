@@ -393,3 +393,102 @@ for _name, _fn in (("moe_route", _moe_route_impl), ("moe_group", _moe_group_impl
                    ("moe_down_q4", _moe_down_q4_impl), ("gemv_f32", _gemv_f32_impl),
                    ("moe_expert_lists", _moe_expert_lists_impl)):
     _LIB.impl(_name, _fn, "CUDA")
+
+
+# ---- Llama decode step: fused norms, embedding, attention, lm_head + argmax -----------------------------------------
+
+HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax keys of the lm_head launch
+
+_LIB.define("rmsnorm_gemv_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) y, int group) -> ()")
+_LIB.define("rmsnorm_gate_up_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) a, int group)"
+            " -> ()")
+_LIB.define("embed_f16(Tensor table, Tensor token, Tensor(a!) x) -> ()")
+_LIB.define("attn_decode(Tensor qkv, Tensor cos, Tensor sin, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor pos, "
+            "int heads, int kv_heads, Tensor(c!) out) -> ()")
+_LIB.define("head_argmax_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) logits, int group, "
+            "Tensor(b!) cand, Tensor(c!) token, Tensor(d!) pos, Tensor(e!) hist, int advance) -> ()")
+
+
+def _q4_shape(wq, ws, group):
+    _u32(wq, "wq")
+    _f16bits(ws, "ws")
+    n, kw = wq.shape
+    k = kw * 8
+    _check(k % group == 0 and ws.numel() == n * (k // group), "ws must be [N, K/group]")
+    return n, k
+
+
+def _rmsnorm_gemv_q4_impl(wq, ws, x, norm_w, eps, y, group):
+    _dev(wq, ws, x, norm_w, y)
+    n, k = _q4_shape(wq, ws, group)
+    _f16bits(norm_w, "norm_w")
+    _check(x.dtype == torch.float32 and y.dtype == torch.float32, "x and y must be float32")
+    tokens = x.numel() // k
+    _check(x.numel() == tokens * k and y.numel() == tokens * n and norm_w.numel() == k, "x [T, K], y [T, N], norm_w [K]")
+    _lib.call("aq_rmsnorm_gemv_q4", _ptr(wq), _ptr(ws), _ptr(x), _ptr(norm_w), eps, _ptr(y), n, k, group, tokens,
+              _stream(x))
+
+
+def _rmsnorm_gate_up_q4_impl(wq, ws, x, norm_w, eps, a, group):
+    _dev(wq, ws, x, norm_w, a)
+    rows, k = _q4_shape(wq, ws, group)
+    _f16bits(norm_w, "norm_w")
+    _check(rows % 2 == 0, "gate|up matrix must have 2f rows")
+    f = rows // 2
+    _check(x.dtype == torch.float32 and a.dtype == torch.float32, "x and a must be float32")
+    tokens = x.numel() // k
+    _check(x.numel() == tokens * k and a.numel() == tokens * f and norm_w.numel() == k, "x [T, K], a [T, f], norm_w [K]")
+    _lib.call("aq_rmsnorm_gate_up_q4", _ptr(wq), _ptr(ws), _ptr(x), _ptr(norm_w), eps, _ptr(a), f, k, group, tokens,
+              _stream(x))
+
+
+def _embed_f16_impl(table, token, x):
+    _dev(table, token, x)
+    _f16bits(table, "table")
+    _check(token.dtype == torch.int32 and token.numel() >= 1, "token must be int32 on the device")
+    _check(x.dtype == torch.float32 and table.dim() == 2 and x.numel() == table.shape[1], "x must be float32 [d]")
+    _lib.call("aq_embed_f16", _ptr(table), table.shape[0], table.shape[1], _ptr(token), _ptr(x), _stream(x))
+
+
+def _attn_decode_impl(qkv, cos, sin, k_cache, v_cache, pos, heads, kv_heads, out):
+    _dev(qkv, cos, sin, k_cache, v_cache, pos, out)
+    _check(qkv.dtype == torch.float32 and out.dtype == torch.float32, "qkv and out must be float32")
+    _check(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin must be float32")
+    _f16bits(k_cache, "k_cache")
+    _f16bits(v_cache, "v_cache")
+    _check(pos.dtype == torch.int32 and pos.numel() >= 1, "pos must be int32 on the device")
+    _check(k_cache.dim() == 3 and k_cache.shape[0] == kv_heads and k_cache.shape[2] == 64, "k_cache [kv_heads, P, 64]")
+    max_pos = k_cache.shape[1]
+    _check(tuple(v_cache.shape) == tuple(k_cache.shape), "v_cache must match k_cache")
+    _check(qkv.numel() == (heads + 2 * kv_heads) * 64 and out.numel() == heads * 64, "qkv/out sizes")
+    _check(cos.numel() == max_pos * 32 and sin.numel() == max_pos * 32, "cos/sin must be [max_pos, 32]")
+    _lib.call("aq_attn_decode", _ptr(qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(pos), heads,
+              kv_heads, 64, max_pos, _ptr(out), _stream(qkv))
+
+
+def _head_argmax_q4_impl(wq, ws, x, norm_w, eps, logits, group, cand, token, pos, hist, advance):
+    _dev(wq, ws, x, logits, cand, token, pos)
+    vocab, k = _q4_shape(wq, ws, group)
+    _check(x.dtype == torch.float32 and x.numel() == k, "x must be float32 [K]")
+    _check(logits.dtype == torch.float32 and logits.numel() == vocab, "logits must be float32 [vocab]")
+    _check(cand.dtype in (torch.int64, torch.uint64), "cand must be 64-bit")
+    _check(token.dtype == torch.int32 and pos.dtype == torch.int32, "token and pos must be int32")
+    nw = 0
+    if norm_w.numel():
+        _dev(norm_w)
+        _f16bits(norm_w, "norm_w")
+        _check(norm_w.numel() == k, "norm_w must be [K]")
+        nw = _ptr(norm_w)
+    hp = 0
+    if hist.numel():
+        _dev(hist)
+        _check(hist.dtype == torch.int32, "hist must be int32")
+        hp = _ptr(hist)
+    _lib.call("aq_head_argmax_q4", _ptr(wq), _ptr(ws), _ptr(x), nw, eps, _ptr(logits), vocab, k, group, _ptr(cand),
+              cand.numel(), _ptr(token), _ptr(pos), hp, hist.numel(), advance, _stream(x))
+
+
+for _name, _fn in (("rmsnorm_gemv_q4", _rmsnorm_gemv_q4_impl), ("rmsnorm_gate_up_q4", _rmsnorm_gate_up_q4_impl),
+                   ("embed_f16", _embed_f16_impl), ("attn_decode", _attn_decode_impl),
+                   ("head_argmax_q4", _head_argmax_q4_impl)):
+    _LIB.impl(_name, _fn, "CUDA")

@@ -1,7 +1,8 @@
 """Seeded synthetic inputs for the benchmark configurations (numpy ``default_rng``; no checkpoints are used).
 
 C0 int4 decode GEMV (Llama-3.2-1B FFN up, 8192 x 2048), C1 int4 prefill GEMM (Llama-3.2-1B projections, M = 431),
-C2 ternary GEMV/GEMM (Qwen3-8B shapes), C3 Qwen3-30B-A3B MoE layer (128 experts, top 8). Weight values follow the
+C2 ternary GEMV/GEMM (Qwen3-8B shapes), C3 Qwen3-30B-A3B MoE layer (128 experts, top 8), C4 Llama-3.2-1B decode
+step (``llama_arrays``; the benchmark draws the full-size model on the device, ``aq.llama.LlamaWeights.random``). Weight values follow the
 stated distributions: int4 offset-8 values uniform in 0..15 (the stored nibble ``q ^ 8`` is then uniform too, so
 the packed words are uniform 32-bit integers), fp16 scales ``|N(0, 0.02)| + 1e-3`` per 32-weight group; ternary
 codes uniform in {0, 1, 2} with fp16 scales ``|N(0, 0.02)|`` per 128.
@@ -77,3 +78,23 @@ def c3(seed: int = 3, tokens: int = C3_TOKENS, experts: int = 128, hidden: int =
     dn_q, dn_s = int4_matrix(rng, experts * hidden, ffn, group)
     return dict(logits=logits, x=x, gu_q=gu_q, gu_s=gu_s, dn_q=dn_q, dn_s=dn_s, experts=experts, hidden=hidden,
                 ffn=ffn, group=group, tokens=tokens)
+
+
+def llama_arrays(cfg, seed: int = 4) -> dict:
+    """Host arrays of a random Llama model of shape ``cfg`` (an ``aq.llama.LlamaConfig``), in the names
+    ``aq.llama.LlamaWeights.from_numpy`` takes: int4 linears as ``int4_matrix``, fp16 norm weights N(1, 0.1), fp16
+    embedding N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    d, f = cfg.dim, cfg.ffn
+    a = {"embed": rng.standard_normal((cfg.vocab, d), dtype=np.float32).astype(np.float16)}
+    norm = lambda: (1 + 0.1 * rng.standard_normal(d, dtype=np.float32)).astype(np.float16)  # noqa: E731
+    for i in range(cfg.layers):
+        p = f"l{i}."
+        a[p + "attn_norm"] = norm()
+        a[p + "mlp_norm"] = norm()
+        for name, (n, k) in (("wqkv", (cfg.qkv, d)), ("wo", (d, cfg.heads * cfg.head_dim)), ("wgu", (2 * f, d)),
+                             ("wdown", (d, f))):
+            a[p + name + ".q"], a[p + name + ".s"] = int4_matrix(rng, n, k, cfg.group)
+    a["final_norm"] = norm()
+    a["lm.q"], a["lm.s"] = int4_matrix(rng, cfg.vocab, d, cfg.group)
+    return a

@@ -10,10 +10,40 @@ namespace aq {
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+// Cross-lane moves by DPP (a VALU operand modifier: no LDS round trip). CTRL: quad_perm 0x00-0xFF, row_mirror 0x140,
+// row_half_mirror 0x141, row_ror:n 0x120 + n, row_bcast:15 0x142, row_bcast:31 0x143 (rows are 16 lanes).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF,
+                                                    false));
+}
+
+// Sum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(0.f, v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp<0x4E>(0.f, v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp<0x141>(0.f, v);  // row_half_mirror: the other quad of the 8
   return v;
+}
+
+// Sum / max over the wave, in every lane: within rows by DPP, across the four rows by row_bcast into the last row,
+// read back from lane 63.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = sum8(v);
+  v += dpp<0x140>(0.f, v);       // row_mirror: the other 8 of the row
+  v += dpp<0x142, 0xA>(0.f, v);  // rows 1, 3 += last lane of rows 0, 2
+  v += dpp<0x143, 0xC>(0.f, v);  // rows 2, 3 += lane 31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v, v));
+  v = fmaxf(v, dpp<0x4E>(v, v));
+  v = fmaxf(v, dpp<0x141>(v, v));
+  v = fmaxf(v, dpp<0x140>(v, v));
+  v = fmaxf(v, dpp<0x142, 0xA>(v, v));
+  v = fmaxf(v, dpp<0x143, 0xC>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
@@ -43,6 +73,22 @@ __device__ __forceinline__ float dot8_biased(uint32_t word, const float* x) {
   d = fmaf((float)(lo >> 24), x[6], d);
   d = fmaf((float)(hi >> 24), x[7], d);
   return d;
+}
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zero (no branch needed).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource used here: the load returns zero
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return half_bits_to_float(h);
 }
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }

@@ -15,22 +15,6 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
 }
 
-// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zero (no branch needed).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource used here: the load returns zero
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return __builtin_bit_cast(uint4, v);
-}
-
-__device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-  return half_bits_to_float(h);
-}
-
 enum { kQ4 = 0, kT2 = 1 };  // weight formats: Q4W rows [N, K/8] / T2W transposed words [K/16, N]
 
 // Kernel arguments (by value). Dense: X [M, K] -> y [M, N]. Grouped (MoE): work tile `it` of tiles[] is (expert e,

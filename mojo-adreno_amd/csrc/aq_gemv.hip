@@ -25,43 +25,260 @@ struct MoeArgs {
   int add;
 };
 
-// G32: the group size is a multiple of 32 (one scale per 32-weight chunk). Otherwise every word looks up its own.
-template <bool G32, int R, int T, int MODE>
+// Decode-step fusions. norm != NULL: every token's x is RMS-normalised on staging, x * (1 / sqrt(mean(x^2) + eps))
+// * norm[k] (fp16 weights), so no separate norm kernel runs before the product. cand != NULL (kStore, one token):
+// each wave also leaves the largest output it wrote and its row, as an argmax key (cand[block * 4 + wave]).
+struct Fuse {
+  const uint16_t* norm;
+  float eps;
+  uint64_t* cand;
+};
+
+// Argmax key: larger for a larger value and, among equal values, for a smaller index, so the maximum key names the
+// first maximum (the reference's `if logits[i] > logits[best]` scan). 0 is below every key of a finite value.
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)idx;
+}
+
+// Weight row r of the output block starting at `base` (every mode but kMoeDown; -1 = no row, kMoeGateUp only). Rows
+// past the end repeat the last output's; their sums are not written.
+template <int MODE, int RO>
+__device__ __forceinline__ int gemv_row(int base, int r, int n_out, int f, const MoeArgs& moe) {
+  int o = base + (r % RO);
+  o = o < n_out ? o : n_out - 1;
+  if constexpr (MODE == kMoeGateUp) {
+    const int e = o / f, j = o - e * f;
+    const int ex = moe.ids[e];
+    return (ex >= 0 && ex < moe.experts) ? ex * 2 * f + j + (r >= RO ? f : 0) : -1;
+  } else {
+    return (MODE == kGateUp && r >= RO) ? f + o : o;
+  }
+}
+
+// G32: the group size is a power of two >= 32 (one scale per 32-weight chunk). Otherwise every word looks up its own.
+// D: register sets of the chunk pipeline (dense G32 modes), chosen at launch from the chunks a wave has.
+template <bool G32, int R, int T, int MODE, int D>
 __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
-                                                 int k, int group, int f, int tokens, MoeArgs moe) {
+                                                 int k, int group, int f, int tokens, MoeArgs moe, Fuse fz) {
   // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots):
   //   xs4[t][p][c]  float4 p = 2j + h holds x[t, 32c + 8j + 4h .. + 3]  (T * 8 planes of nch float4)
   //   xsum[t][j][c] sum of x[t, 32c + 8j .. + 7]                        (T * 4 planes of nch floats)
   extern __shared__ float4 lds4[];
+  __shared__ float red[4 * T];
   const int kw = k >> 3;
   const int nch = k >> 5;
   float4* xs4 = lds4;
   float* xsum = reinterpret_cast<float*>(lds4 + T * 8 * nch);
-  for (int i = threadIdx.x; i < T * kw; i += 256) {
-    const int t = i / kw;
-    const int wi = i - t * kw;
-    const int c = wi >> 2;
-    const int j = wi & 3;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-    if (t < tokens) {
-      const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
-      a = src[0];
-      b = src[1];
-    }
-    xs4[(t * 8 + 2 * j) * nch + c] = a;
-    xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
-    xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-  }
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int gpr = k / group;
   constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
   constexpr int SL = MODE == kMoeDown ? T : 1;  // weight rows per output (kMoeDown: one per expert slot)
+  // G32 dense products (kStore, kAdd, kGateUp) stream the wave's chunks, over all its row blocks, through D register
+  // sets: D chunks are in flight while one is used (with D > 1 the last D requests fall past the end and carry an
+  // out-of-range offset; with D = 1 nothing is requested past the end). kMoeGateUp (rows from device expert ids)
+  // double-buffers within a row block. The rest (kMoeDown, groups that are not powers of two >= 32) request each chunk
+  // when they use it.
+  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp);
+  constexpr bool kPipe = G32 && MODE == kMoeGateUp;
+  const int stride = gridDim.x * 4 * RO;
+  const int cpl = (nch + kWave - 1) / kWave;  // chunks per lane and row block (the last may be partial)
 
-  for (int base = (blockIdx.x * 4 + wave) * RO; base < n_out; base += gridDim.x * 4 * RO) {
+  // one chunk (16 bytes = 32 weights of each of the R rows, and their G32 scales); only kMoeGateUp can name no row
+  // (an invalid expert id): its weights read as zero codes with scale 0
+  // scales travel as raw fp16 bits and are converted where used: a conversion next to its load would wait for it
+  const int gsh = __builtin_ctz(group);  // G32 groups are powers of two
+  auto load_chunk = [&](const int (&rows)[R], int c, uint4 (&w)[R], uint16_t (&sc)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool ok = MODE != kMoeGateUp || rows[r] >= 0;
+      w[r] = ok ? *reinterpret_cast<const uint4*>(wq + (size_t)rows[r] * kw + c * 4)
+                : make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+      sc[r] = ok ? ws[(size_t)rows[r] * gpr + ((c * 32) >> gsh)] : (uint16_t)0;
+    }
+  };
+  auto use_chunk = [&](int c, const uint4 (&w)[R], const uint16_t (&sc)[R], float (&acc)[R][T]) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float* s4 = xsum + t * 4 * nch + c;
+      const float xs32 = (s4[0] + s4[nch]) + (s4[2 * nch] + s4[3 * nch]);
+      float part[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[r] = -8.0f * xs32;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float xv[8];
+        *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
+        *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
+          part[r] += dot8_biased(wj, xv);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]), acc[r][t]);
+    }
+  };
+
+  // The first chunk of this wave's first row block is requested before x is staged, so its latency overlaps the
+  // staging instead of following it.
+  const int base0 = (blockIdx.x * 4 + wave) * RO;
+  uint4 wd[D][R];
+  uint32_t sd[D][R];  // the aligned 4 bytes holding each scale (fp16 pairs)
+  uint32_t sh[D][R];  // ... and the scale's bit offset in them (0 or 16)
+  // kDeep reads W and scales and writes y through buffer resources: a chunk past the wave's last row block, a tail
+  // lane past K, or a lane that stores nothing issues its instruction with an out-of-range offset (no traffic, no
+  // branch). Every chunk is then the same 2R loads, so the compiler's wait counts see the full pipeline depth.
+  const int wrows = MODE == kGateUp ? 2 * f : n_out;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)wrows * kw * 4));
+  // scales are read as the aligned 4 bytes holding them (a 16-bit load would be widened right after it, waiting for
+  // it); the range is rounded up to whole 4-byte words, so an odd count's last scale is read with the 2 bytes after it
+  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)(((size_t)wrows * gpr * 2 + 3) & ~(size_t)3));
+  const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(y, (uint32_t)((size_t)tokens * n_out * 4));
+  int ib = base0, ic = 0;  // kDeep: the next chunk to request (row block, chunk index)
+  auto issue_next = [&](uint4 (&w)[R], uint32_t (&sc)[R], uint32_t (&sb)[R]) {
+    const uint32_t c = lane + ic * kWave;
+    const bool ok = ib < n_out && c < (uint32_t)nch;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t row = gemv_row<MODE, RO>(ib, r, n_out, f, moe);  // a valid row even past the end
+      const uint32_t wo = (row * (uint32_t)kw + 4 * c) * 4;
+      const uint32_t si = row * (uint32_t)gpr + ((32 * c) >> gsh);
+      w[r] = buf_load16(w_rsrc, ok ? wo : kOOB);
+      sc[r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, ok ? (si * 2) & ~3u : kOOB, 0, 0);
+      sb[r] = (si & 1) << 4;
+    }
+    if (ib < n_out && ++ic == cpl) ic = 0, ib += stride;
+  };
+  if constexpr (kDeep) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue_next(wd[d], sd[d], sh[d]);
+  }
+  uint4 wa[R], wb[R];
+  uint16_t sa[R], sb[R];
+  if constexpr (kPipe) {
+    if (base0 < n_out && lane < nch) {
+      int rows0[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) rows0[r] = gemv_row<MODE, RO>(base0, r, n_out, f, moe);
+      load_chunk(rows0, lane, wa, sa);
+    }
+  }
+
+  // Stage x in one pass. With a norm, x * norm_w is staged and sum(x^2) gathered on the way; the row sums are then
+  // scaled by 1 / sqrt(mean(x^2) + eps) (a per-token scalar), which is the RMSNorm'd product.
+  float ss[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    ss[t] = 0.f;
+    for (int wi = threadIdx.x; wi < kw; wi += 256) {
+      const int c = wi >> 2;
+      const int j = wi & 3;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if (t < tokens) {
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
+        a = src[0];
+        b = src[1];
+        if (fz.norm) {  // workgroup-uniform
+          ss[t] += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
+                   ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+          const uint4 wn = *reinterpret_cast<const uint4*>(fz.norm + wi * 8);
+          a.x *= half_bits_to_float(wn.x & 0xFFFF);
+          a.y *= half_bits_to_float(wn.x >> 16);
+          a.z *= half_bits_to_float(wn.y & 0xFFFF);
+          a.w *= half_bits_to_float(wn.y >> 16);
+          b.x *= half_bits_to_float(wn.z & 0xFFFF);
+          b.y *= half_bits_to_float(wn.z >> 16);
+          b.z *= half_bits_to_float(wn.w & 0xFFFF);
+          b.w *= half_bits_to_float(wn.w >> 16);
+        }
+      }
+      xs4[(t * 8 + 2 * j) * nch + c] = a;
+      xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
+      xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    }
+  }
+  if (fz.norm) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float v = wave_sum(ss[t]);
+      if (lane == 0) red[wave * T + t] = v;
+    }
+  }
+  __syncthreads();
+  float rs[T];  // per-token RMSNorm scale (1 without a norm)
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    rs[t] = fz.norm ? 1.0f / sqrtf(((red[t] + red[T + t]) + (red[2 * T + t] + red[3 * T + t])) / (float)k + fz.eps)
+                    : 1.0f;
+
+  float best = 0.f;  // argmax candidate of this wave (kStore, token 0)
+  int best_row = -1;
+
+  // the row sums of one row block: scaled by the norm, stored (or added, or combined as silu(gate) * up) by lane 0;
+  // the other lanes' accesses carry an out-of-range offset
+  auto finish = [&](int base, float (&acc)[R][T]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[r][t] = wave_sum(acc[r][t]) * rs[t];
+#pragma unroll
+    for (int r = 0; r < RO; ++r) {
+      const int o = base + r;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint32_t off = (lane == 0 && o < n_out && t < tokens) ? ((uint32_t)t * n_out + o) * 4 : kOOB;
+        float v = acc[r][t];
+        if constexpr (MODE == kGateUp || MODE == kMoeGateUp) v = silu(v) * acc[RO + r][t];
+        if constexpr (MODE == kAdd) v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+      }
+      if constexpr (MODE == kStore) {  // rows arrive in ascending order, so `>` keeps the first maximum
+        if (o < n_out && (best_row < 0 || acc[r][0] > best)) best = acc[r][0], best_row = o;
+      }
+    }
+  };
+
+  if constexpr (kDeep) {
+    float acc[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
+    int cb = base0, cc = 0;  // the chunk to use next
+    bool more = cb < n_out;
+    while (more) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {  // register set d by name: set d always holds the chunk d steps ahead
+        if (more) {
+          const int c = lane + cc * kWave;
+          if (c < nch) {
+            uint16_t s16[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) s16[r] = (uint16_t)(sd[d][r] >> sh[d][r]);
+            use_chunk(c, wd[d], s16, acc);
+          }
+          if (D > 1 || cb + (cc + 1 == cpl ? stride : 0) < n_out) issue_next(wd[d], sd[d], sh[d]);
+          if (++cc == cpl) {
+            finish(cb, acc);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
+            cc = 0;
+            cb += stride;
+            more = cb < n_out;
+          }
+        }
+      }
+    }
+  }
+
+  for (int base = base0; kDeep ? false : base < n_out; base += stride) {
     int rows[R][SL];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -69,15 +286,11 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       o = o < n_out ? o : n_out - 1;  // rows past the end repeat the last one; their sums are not written
 #pragma unroll
       for (int sl = 0; sl < SL; ++sl) {
-        if constexpr (MODE == kMoeGateUp) {
-          const int e = o / f, j = o - e * f;
-          const int ex = moe.ids[e];
-          rows[r][sl] = (ex >= 0 && ex < moe.experts) ? ex * 2 * f + j + (r >= RO ? f : 0) : -1;
-        } else if constexpr (MODE == kMoeDown) {
+        if constexpr (MODE == kMoeDown) {
           const int ex = sl < tokens ? moe.ids[sl] : -1;
           rows[r][sl] = (ex >= 0 && ex < moe.experts) ? ex * n_out + o : -1;
         } else {
-          rows[r][sl] = (MODE == kGateUp && r >= RO) ? f + o : o;
+          rows[r][sl] = gemv_row<MODE, RO>(base, r, n_out, f, moe);
         }
       }
     }
@@ -87,96 +300,83 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
 
-    for (int c = lane; c < nch; c += kWave) {
-      if constexpr (MODE == kMoeDown) {
-        // one row per expert slot t, applied to that slot's activations only
+    if constexpr (kPipe) {
+      int rw[R];
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const int row = rows[0][t];
-          if (row < 0) continue;  // wave-uniform
-          const uint4 w4 = *reinterpret_cast<const uint4*>(wq + (size_t)row * kw + c * 4);
-          const uint32_t wv4[4] = {w4.x, w4.y, w4.z, w4.w};
-          float part = 0.f;
-          if constexpr (G32) {
-            const float* s4 = xsum + t * 4 * nch + c;
-            part = -8.0f * ((s4[0] + s4[nch]) + (s4[2 * nch] + s4[3 * nch]));
-          }
+      for (int r = 0; r < R; ++r) rw[r] = rows[r][0];
+      if (base != base0 && lane < nch) load_chunk(rw, lane, wa, sa);  // the first block's came before staging
+      // two register sets used in turn by name (a copy of a set still in flight would wait for it)
+      for (int c = lane; c < nch; c += 2 * kWave) {
+        const bool more1 = c + kWave < nch;
+        if (more1) load_chunk(rw, c + kWave, wb, sb);
+        use_chunk(c, wa, sa, acc);
+        if (!more1) break;
+        const bool more2 = c + 2 * kWave < nch;
+        if (more2) load_chunk(rw, c + 2 * kWave, wa, sa);
+        use_chunk(c + kWave, wb, sb, acc);
+        if (!more2) break;
+      }
+    } else {
+      for (int c = lane; c < nch; c += kWave) {
+        if constexpr (MODE == kMoeDown) {
+          // one row per expert slot t, applied to that slot's activations only
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float xv[8];
-            *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
-            *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
+          for (int t = 0; t < T; ++t) {
+            const int row = rows[0][t];
+            if (row < 0) continue;  // wave-uniform
+            const uint4 w4 = *reinterpret_cast<const uint4*>(wq + (size_t)row * kw + c * 4);
+            const uint32_t wv4[4] = {w4.x, w4.y, w4.z, w4.w};
+            float part = 0.f;
             if constexpr (G32) {
-              part += dot8_biased(wv4[j], xv);
-            } else {
-              const float sj = half_bits_to_float(ws[(size_t)row * gpr + (c * 32 + 8 * j) / group]);
-              part = fmaf(dot8_biased(wv4[j], xv) - 8.0f * xsum[(t * 4 + j) * nch + c], sj, part);
+              const float* s4 = xsum + t * 4 * nch + c;
+              part = -8.0f * ((s4[0] + s4[nch]) + (s4[2 * nch] + s4[3 * nch]));
             }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              float xv[8];
+              *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
+              *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
+              if constexpr (G32) {
+                part += dot8_biased(wv4[j], xv);
+              } else {
+                const float sj = half_bits_to_float(ws[(size_t)row * gpr + (c * 32 + 8 * j) / group]);
+                part = fmaf(dot8_biased(wv4[j], xv) - 8.0f * xsum[(t * 4 + j) * nch + c], sj, part);
+              }
+            }
+            if constexpr (G32) part *= half_bits_to_float(ws[(size_t)row * gpr + (c * 32) / group]);
+            acc[0][t] += part;
           }
-          if constexpr (G32) part *= half_bits_to_float(ws[(size_t)row * gpr + (c * 32) / group]);
-          acc[0][t] += part;
-        }
-        continue;
-      }
-      // only kMoeGateUp can name no row (an invalid expert id): its weights read as zero codes with scale 0
-      uint4 wv[R];
+        } else {  // a group smaller than 32 or not a multiple of it: one scale per 8-weight word
+          uint4 wv[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (MODE != kMoeGateUp || rows[r][0] >= 0)
-          wv[r] = *reinterpret_cast<const uint4*>(wq + (size_t)rows[r][0] * kw + c * 4);
-        else
-          wv[r] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-      }
-      if constexpr (G32) {
-        const int gi = (c * 32) / group;
-        float sc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          sc[r] = (MODE != kMoeGateUp || rows[r][0] >= 0) ? half_bits_to_float(ws[(size_t)rows[r][0] * gpr + gi])
-                                                           : 0.f;
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const float* sc4 = xsum + t * 4 * nch + c;
-          const float xs32 = (sc4[0] + sc4[nch]) + (sc4[2 * nch] + sc4[3 * nch]);
-          float part[R];
-#pragma unroll
-          for (int r = 0; r < R; ++r) part[r] = -8.0f * xs32;
+          for (int r = 0; r < R; ++r) {
+            if (MODE != kMoeGateUp || rows[r][0] >= 0)
+              wv[r] = *reinterpret_cast<const uint4*>(wq + (size_t)rows[r][0] * kw + c * 4);
+            else
+              wv[r] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+          }
+          float sc[R][4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            float xv[8];
-            *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
-            *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
+            const int gi = (c * 32 + 8 * j) / group;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-              const uint32_t w = j == 0 ? wv[r].x : j == 1 ? wv[r].y : j == 2 ? wv[r].z : wv[r].w;
-              part[r] += dot8_biased(w, xv);
-            }
+            for (int r = 0; r < R; ++r)
+              sc[r][j] = (MODE != kMoeGateUp || rows[r][0] >= 0)
+                             ? half_bits_to_float(ws[(size_t)rows[r][0] * gpr + gi]) : 0.f;
           }
 #pragma unroll
-          for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], sc[r], acc[r][t]);
-        }
-      } else {
-        float sc[R][4];
+          for (int t = 0; t < T; ++t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int gi = (c * 32 + 8 * j) / group;
+            for (int j = 0; j < 4; ++j) {
+              float xv[8];
+              *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
+              *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
+              const float xs8 = xsum[(t * 4 + j) * nch + c];
 #pragma unroll
-          for (int r = 0; r < R; ++r)
-            sc[r][j] = (MODE != kMoeGateUp || rows[r][0] >= 0)
-                           ? half_bits_to_float(ws[(size_t)rows[r][0] * gpr + gi]) : 0.f;
-        }
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float xv[8];
-            *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
-            *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
-            const float xs8 = xsum[(t * 4 + j) * nch + c];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-              const uint32_t w = j == 0 ? wv[r].x : j == 1 ? wv[r].y : j == 2 ? wv[r].z : wv[r].w;
-              acc[r][t] = fmaf(dot8_biased(w, xv) - 8.0f * xs8, sc[r][j], acc[r][t]);
+              for (int r = 0; r < R; ++r) {
+                const uint32_t w = j == 0 ? wv[r].x : j == 1 ? wv[r].y : j == 2 ? wv[r].z : wv[r].w;
+                acc[r][t] = fmaf(dot8_biased(w, xv) - 8.0f * xs8, sc[r][j], acc[r][t]);
+              }
             }
           }
         }
@@ -191,86 +391,126 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       if (lane == 0) y[base] = moe.add ? y[base] + sum : sum;
       continue;
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < T; ++t) acc[r][t] = wave_sum(acc[r][t]);
-
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < RO; ++r) {
-        const int o = base + r;
-        if (o >= n_out) break;
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          if (t >= tokens) break;
-          float* dst = y + (size_t)t * n_out + o;
-          if constexpr (MODE == kStore) *dst = acc[r][t];
-          else if constexpr (MODE == kAdd) *dst += acc[r][t];
-          else *dst = silu(acc[r][t]) * acc[RO + r][t];
-        }
-      }
-    }
+    finish(base, acc);
+  }
+  if constexpr (MODE == kStore) {
+    if (fz.cand && lane == 0) fz.cand[blockIdx.x * 4 + wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
   }
 }
 
-template <bool G32, int R, int T, int MODE>
-static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
-                    int f, int tokens, const MoeArgs& moe, hipStream_t s) {
+// Workgroups of a launch over n_out outputs, RO per wave: one pass of 4 waves each, at most 1024 (then grid-stride).
+inline int gemv_blocks(int64_t n_out, int ro) {
+  const int64_t b = (n_out + 4 * ro - 1) / (4 * ro);
+  return b > 1024 ? 1024 : (int)b;
+}
+
+template <bool G32, int R, int T, int MODE, int D>
+static int launch_d(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
+                    int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
   constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
   const size_t lds = (size_t)T * k * sizeof(float) + (size_t)T * (k / 8) * sizeof(float);
-  auto kern = k_gemv_q4<G32, R, T, MODE>;
+  auto kern = k_gemv_q4<G32, R, T, MODE, D>;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
       return AQ_ERR_CAPACITY;
   }
-  int blocks = (n_out + 4 * RO - 1) / (4 * RO);
-  if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, wq, ws, x, y, n_out, k, group, f, tokens, moe);
+  const int blocks = gemv_blocks(n_out, RO);
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, wq, ws, x, y, n_out, k, group, f, tokens, moe, fz);
   return launch_status();
+}
+
+// Pipeline depth of the dense G32 modes: the chunks one wave streams (per lane: K/2048 per row block, times its row
+// blocks), at most 2 register sets of 4 rows or 4 of 2. One chunk (most decode shapes) runs unpipelined.
+template <bool G32, int R, int T, int MODE>
+static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
+                    int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
+  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp);
+  if constexpr (kDeep) {
+    constexpr int RO = MODE == kGateUp ? R / 2 : R;
+    const int64_t waves = 4 * (int64_t)gemv_blocks(n_out, RO);
+    const int64_t items = ((k / 32 + 63) / 64) * ((n_out + waves * RO - 1) / (waves * RO));
+    if (items >= 4 && R <= 2) return launch_d<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    if (items >= 2) return launch_d<G32, R, T, MODE, 2>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  }
+  return launch_d<G32, R, T, MODE, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
 }
 
 // Weight rows per wave iteration. Measured on MI355X (G = 32, K = 2048): R = 2 is fastest while the matrix has fewer
 // than 16K rows (N = 5120: 4.5 us vs 5.3 us at R = 4; N = 8192: 5.0 vs 5.5 us; N = 2048, K = 8192: 7.6 vs 9.9 us),
 // R = 4 from 16K rows on (N = 16384: 7.3 vs 7.4 us; N = 128256: 35.3 vs 38.1 us). kMoeDown reads one row per expert
 // slot for each output instead.
+inline int rows_per_wave(int64_t rows) { return rows < 16384 ? 2 : 4; }
+
 template <bool G32, int T, int MODE>
 static int launch_r(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
-                    int f, int tokens, const MoeArgs& moe, hipStream_t s) {
+                    int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
   if constexpr (MODE == kMoeDown) {
-    return launch_t<G32, 1, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
+    return launch_t<G32, 1, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   } else {
     const int64_t rows = (MODE == kGateUp || MODE == kMoeGateUp) ? 2 * (int64_t)n_out : n_out;
-    if (rows < 16384) return launch_t<G32, 2, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
-    return launch_t<G32, 4, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
+    if (rows_per_wave(rows) == 2) return launch_t<G32, 2, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    return launch_t<G32, 4, T, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   }
 }
 
 template <bool G32, int MODE>
 static int launch_g(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
-                    int f, int tokens, const MoeArgs& moe, hipStream_t s) {
-  if (tokens <= 1) return launch_r<G32, 1, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
-  if (tokens <= 2) return launch_r<G32, 2, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
-  if (tokens <= 4) return launch_r<G32, 4, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
-  return launch_r<G32, 8, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, s);
+                    int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
+  if (tokens <= 1) return launch_r<G32, 1, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  if (tokens <= 2) return launch_r<G32, 2, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  if (tokens <= 4) return launch_r<G32, 4, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  return launch_r<G32, 8, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
 }
 
 template <int MODE>
 static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int64_t n_out, int64_t k,
-                      int32_t group, int64_t f, int32_t tokens, const MoeArgs& moe, void* stream) {
+                      int32_t group, int64_t f, int32_t tokens, const MoeArgs& moe, void* stream,
+                      const Fuse& fz = Fuse{nullptr, 0.f, nullptr}) {
   if (!wq || !ws || !x || !y) return AQ_ERR_NULL;
+  if (fz.norm && !aligned(fz.norm, 16)) return AQ_ERR_ALIGN;
   if (n_out <= 0 || k <= 0 || tokens < 1 || tokens > 8) return AQ_ERR_SHAPE;
   if (k % 32) return AQ_ERR_SHAPE;
   if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
   const int tp = tokens <= 1 ? 1 : tokens <= 2 ? 2 : tokens <= 4 ? 4 : 8;
   if ((int64_t)tp * k > 32768) return AQ_ERR_CAPACITY;
   if (n_out > (int64_t)1 << 30) return AQ_ERR_SHAPE;
+  // W, its scales and y are addressed through 32-bit buffer offsets below 2 GiB
+  const int64_t wrows = (MODE == kGateUp || MODE == kMoeGateUp) ? 2 * n_out : n_out;
+  if (wrows * k / 2 >= ((int64_t)1 << 31) || (int64_t)tokens * n_out * 4 >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
   if (!aligned(wq, 16) || !aligned(x, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (group % 32 == 0)
-    return launch_g<true, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, s);
-  return launch_g<false, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, s);
+  if (group >= 32 && (group & (group - 1)) == 0)
+    return launch_g<true, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
+  return launch_g<false, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
+}
+
+// Greedy-decode step end: the maximum of ncand argmax keys names the next token; it is written to *token and to
+// hist[*pos] (when hist_cap > *pos), then *pos advances by `advance`. One workgroup.
+__global__ __launch_bounds__(1024) void k_argmax_step(const uint64_t* __restrict__ cand, int ncand,
+                                                      int32_t* __restrict__ token, int32_t* __restrict__ pos,
+                                                      int32_t* __restrict__ hist, int hist_cap, int advance) {
+  __shared__ uint64_t red[16];
+  uint64_t m = 0;
+  for (int i = threadIdx.x; i < ncand; i += 1024) {
+    const uint64_t c = cand[i];
+    m = c > m ? c : m;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = __shfl_xor(m, d, kWave);
+    m = o > m ? o : m;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w) m = red[w] > m ? red[w] : m;  // m is red[0] here
+    const int idx = m ? (int)~(uint32_t)m : 0;
+    const int p = *pos;
+    *token = idx;
+    if (hist && p >= 0 && p < hist_cap) hist[p] = idx;
+    *pos = p + advance;
+  }
 }
 
 }  // namespace aq
@@ -305,4 +545,39 @@ extern "C" int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t ex
   // the expert slots are the kernel's "tokens": act [topk, f] holds one activation vector per slot
   const aq::MoeArgs moe{ids, weights, (int)experts, add ? 1 : 0};
   return aq::gemv_entry<aq::kMoeDown>(wq, ws, act, y, d, f, group, 0, topk, moe, stream);
+}
+
+extern "C" int aq_rmsnorm_gemv_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
+                                  float eps, float* y, int64_t n, int64_t k, int32_t group, int32_t tokens,
+                                  void* stream) {
+  if (!norm_w) return AQ_ERR_NULL;
+  const aq::MoeArgs none{nullptr, nullptr, 0, 0};
+  return aq::gemv_entry<aq::kStore>(wq, ws, x, y, n, k, group, 0, tokens, none, stream, aq::Fuse{norm_w, eps, nullptr});
+}
+
+extern "C" int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
+                                     float eps, float* a, int64_t f, int64_t k, int32_t group, int32_t tokens,
+                                     void* stream) {
+  if (!norm_w) return AQ_ERR_NULL;
+  const aq::MoeArgs none{nullptr, nullptr, 0, 0};
+  return aq::gemv_entry<aq::kGateUp>(wq, ws, x, a, f, k, group, f, tokens, none, stream,
+                                     aq::Fuse{norm_w, eps, nullptr});
+}
+
+extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
+                                 float eps, float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand,
+                                 int64_t cand_cap, int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap,
+                                 int32_t advance, void* stream) {
+  if (!cand || !token || !pos) return AQ_ERR_NULL;
+  if (vocab <= 0 || vocab > (int64_t)1 << 30 || hist_cap < 0) return AQ_ERR_SHAPE;
+  const int ncand = 4 * aq::gemv_blocks(vocab, aq::rows_per_wave(vocab));
+  if (cand_cap < ncand) return AQ_ERR_CAPACITY;
+  if (!aq::aligned(cand, 8)) return AQ_ERR_ALIGN;
+  const aq::MoeArgs none{nullptr, nullptr, 0, 0};
+  const int st = aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream,
+                                            aq::Fuse{norm_w, eps, cand});
+  if (st != AQ_OK) return st;
+  hipLaunchKernelGGL(aq::k_argmax_step, dim3(1), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), cand, ncand,
+                     token, pos, hist, hist_cap, advance);
+  return aq::launch_status();
 }

@@ -342,6 +342,96 @@ def moe_layer(x, logits, gu_q, gu_s, dn_q, dn_s, group: int, fe: int, topk: int 
 
 
 # ----------------------------------------------------------------------------------------------------------------
+# Llama decode step (embedding, RMSNorm, RoPE, attention over the KV cache, SwiGLU MLP, lm_head, greedy argmax)
+# ----------------------------------------------------------------------------------------------------------------
+
+
+def rmsnorm(x, w, eps: float = 1e-5) -> np.ndarray:
+    """``x / sqrt(mean(x^2) + eps) * w``, float64 (llama/kernels/rmsnorm.mojo:17-35; w fp16)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, dtype=np.float64)
+
+
+def rope(v, cos_p, sin_p) -> np.ndarray:
+    """rotate_half RoPE of head vectors ``v [..., 64]`` at one position: pairs (i, i + 32) ->
+    ``(a c_i - b s_i, b c_i + a s_i)`` (llama/kernels/rope_kv.mojo:27-33), float64."""
+    v = np.asarray(v, dtype=np.float64)
+    h = v.shape[-1] // 2
+    a, b = v[..., :h], v[..., h:]
+    c, s = np.asarray(cos_p, dtype=np.float64), np.asarray(sin_p, dtype=np.float64)
+    return np.concatenate([a * c - b * s, b * c + a * s], axis=-1)
+
+
+def attention_decode(q, kc, vc, n: int) -> np.ndarray:
+    """Grouped-query attention of one token over cache rows s < n: ``out_h = softmax_s(q_h . k_s / sqrt(d)) . v_s`` with
+    KV head h // (H / KVH) (llama/kernels/attention.mojo:19-66). q [H, d], kc/vc [KVH, P, d] -> [H, d], float64."""
+    q = np.asarray(q, dtype=np.float64)
+    heads, d = q.shape
+    kv = kc.shape[0]
+    out = np.empty((heads, d))
+    for h in range(heads):
+        g = h // (heads // kv)
+        k = np.asarray(kc[g, :n], dtype=np.float64)
+        sc = (k @ q[h]) / np.sqrt(d)
+        p = np.exp(sc - sc.max())
+        out[h] = (p @ np.asarray(vc[g, :n], dtype=np.float64)) / p.sum()
+    return out
+
+
+def argmax_first(v) -> int:
+    """The first index of the largest value (llama/llama.mojo:72-75: ``if logits[i] > logits[best]``); numpy's argmax
+    returns the first occurrence of the maximum."""
+    return int(np.argmax(np.asarray(v)))
+
+
+class LlamaDecodeOracle:
+    """One-token-at-a-time Llama decode, float64 on dequantised weights: the forward pass of llama/model.mojo:140-166
+    (embed; per layer rmsnorm, qkv, rope_kv, attention, o + residual, rmsnorm, gate|up, silu_mul, down + residual;
+    final rmsnorm, lm_head). ``kv_dtype`` rounds what the cache stores (np.float16 for an fp16 cache, None to keep
+    float64, as the reference's fp32 cache is for these purposes).
+
+    ``arrays`` as ``aq.llama.LlamaWeights.from_numpy`` takes them; ``cos``/``sin`` [max_pos, d/2] tables."""
+
+    def __init__(self, arrays: dict, cfg, cos, sin, kv_dtype=np.float16):
+        self.cfg, self.cos, self.sin, self.kv_dtype = cfg, np.asarray(cos), np.asarray(sin), kv_dtype
+        g = cfg.group
+        deq = lambda name: q4w_dequant(arrays[name + ".q"], arrays[name + ".s"], g).astype(np.float64)  # noqa: E731
+        self.embed = np.asarray(arrays["embed"], dtype=np.float16)
+        self.layers = []
+        for i in range(cfg.layers):
+            p = f"l{i}."
+            self.layers.append({"attn_norm": np.asarray(arrays[p + "attn_norm"], np.float16),
+                                "mlp_norm": np.asarray(arrays[p + "mlp_norm"], np.float16),
+                                **{m: deq(p + m) for m in ("wqkv", "wo", "wgu", "wdown")}})
+        self.final_norm = np.asarray(arrays["final_norm"], np.float16)
+        self.lm = deq("lm")
+        shape = (cfg.kv_heads, cfg.max_pos, cfg.head_dim)
+        self.kc = [np.zeros(shape) for _ in range(cfg.layers)]
+        self.vc = [np.zeros(shape) for _ in range(cfg.layers)]
+
+    def _store(self, v):
+        return v.astype(self.kv_dtype).astype(np.float64) if self.kv_dtype is not None else v
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        """Logits (float64 [vocab]) of ``token`` at ``pos``; appends this position's keys and values to the cache."""
+        cfg = self.cfg
+        hd, nh, nkv = cfg.head_dim, cfg.heads, cfg.kv_heads
+        x = self.embed[token].astype(np.float64)
+        for i, lw in enumerate(self.layers):
+            qkv = lw["wqkv"] @ rmsnorm(x, lw["attn_norm"], cfg.eps)
+            q = rope(qkv[:nh * hd].reshape(nh, hd), self.cos[pos], self.sin[pos])
+            k = rope(qkv[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), self.cos[pos], self.sin[pos])
+            v = qkv[(nh + nkv) * hd:].reshape(nkv, hd)
+            self.kc[i][:, pos] = self._store(k)
+            self.vc[i][:, pos] = self._store(v)
+            att = attention_decode(q, self.kc[i], self.vc[i], pos + 1)
+            x = x + lw["wo"] @ att.reshape(-1)
+            h = lw["wgu"] @ rmsnorm(x, lw["mlp_norm"], cfg.eps)
+            x = x + lw["wdown"] @ (silu(h[:cfg.ffn]) * h[cfg.ffn:])
+        return self.lm @ rmsnorm(x, self.final_norm, cfg.eps)
+
+
+# ----------------------------------------------------------------------------------------------------------------
 # weight formats (host side)
 # ----------------------------------------------------------------------------------------------------------------
 

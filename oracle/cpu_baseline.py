@@ -75,3 +75,49 @@ def gemm_layer(mats: dict, xs: dict, group: int, reps=5, budget_s=8.0):
             torch.nn.functional.linear(xt[w.shape[1]], w)
 
     return median_time(run, reps, budget_s)
+
+
+def llama_decode(mats: dict, head: tuple, dim: int, heads: int, kv_heads: int, ffn: int, context: int,
+                 group: int, reps=5, budget_s=10.0):
+    """Seconds for one decode step's layers (as many as ``mats`` holds) and for the head, fp32 torch on the CPU over
+    dequantised weights: rmsnorm, fused qkv, RoPE, attention over ``context`` cached positions (fp32 cache), o +
+    residual, rmsnorm, gate|up, SiLU product, down + residual (llama/model.mojo:140-166, the arithmetic run.py checks
+    with transformers). ``mats[layer] = {name: (words, scales)}`` for wqkv, wo, wgu, wdown; ``head`` = lm_head words,
+    scales. Returns (seconds for the layers, seconds for final norm + lm_head + argmax)."""
+    hd = dim // heads
+    lw = [{name: dequant_q4(q, s, group) for name, (q, s) in m.items()} for m in mats]
+    lm = dequant_q4(*head, group)
+    g = torch.Generator().manual_seed(0)
+    kc = [torch.randn(kv_heads, context, hd, generator=g) for _ in lw]
+    vc = [torch.randn(kv_heads, context, hd, generator=g) for _ in lw]
+    nw = torch.ones(dim)
+    cos, sin = torch.rand(hd // 2, generator=g), torch.rand(hd // 2, generator=g)
+    x0 = torch.randn(dim, generator=g)
+    F = torch.nn.functional
+
+    def rms(x):
+        return x * torch.rsqrt((x * x).mean() + 1e-5) * nw
+
+    def rope(v):
+        a, b = v[..., :hd // 2], v[..., hd // 2:]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+
+    def layers():
+        x = x0.clone()
+        for i, w in enumerate(lw):
+            qkv = F.linear(rms(x), w["wqkv"])
+            q = rope(qkv[:heads * hd].view(heads, hd))
+            kc[i][:, -1] = rope(qkv[heads * hd:(heads + kv_heads) * hd].view(kv_heads, hd))
+            vc[i][:, -1] = qkv[(heads + kv_heads) * hd:].view(kv_heads, hd)
+            k = kc[i].repeat_interleave(heads // kv_heads, 0)
+            v = vc[i].repeat_interleave(heads // kv_heads, 0)
+            p = torch.softmax(torch.einsum("hd,hsd->hs", q, k) / hd ** 0.5, dim=-1)
+            x = x + F.linear(torch.einsum("hs,hsd->hd", p, v).reshape(-1), w["wo"])
+            h = F.linear(rms(x), w["wgu"])
+            x = x + F.linear(F.silu(h[:ffn]) * h[ffn:], w["wdown"])
+        return x
+
+    def head_fn():
+        return int(torch.argmax(F.linear(rms(x0), lm)))
+
+    return median_time(layers, reps, budget_s / 2), median_time(head_fn, reps, budget_s / 2)

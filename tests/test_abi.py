@@ -77,3 +77,32 @@ def test_ops_reject_host_tensors():
     wq = torch.zeros((8, 64), dtype=torch.int32)
     with pytest.raises((ValueError, NotImplementedError, RuntimeError)):
         ops.gemv_q4(wq, torch.zeros((8, 16), dtype=torch.float16), torch.zeros(512), torch.zeros(8), 32)
+
+
+def test_decode_entries_reject_bad_arguments_before_launch():
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    f = ctypes.c_float(1e-5)
+    assert lib.aq_rmsnorm_gemv_q4(p, p, p, None, f, p, 8, 512, 32, 1, None) == 5        # no norm weights
+    assert lib.aq_rmsnorm_gemv_q4(p, p, p, p + 2, f, p, 8, 512, 32, 1, None) == 3       # misaligned norm weights
+    assert lib.aq_rmsnorm_gate_up_q4(p, p, p, p, f, p, 8, 500, 32, 1, None) == 1        # K % 32
+    assert lib.aq_embed_f16(p, 100, 12, p, p, None) == 1                                 # d % 8
+    assert lib.aq_embed_f16(None, 100, 16, p, p, None) == 5
+    assert lib.aq_attn_decode(p, p, p, p, p, p, 32, 8, 128, 512, p, None) == 1          # head_dim != 64
+    assert lib.aq_attn_decode(p, p, p, p, p, p, 32, 6, 64, 512, p, None) == 1           # heads % kv_heads
+    assert lib.aq_attn_decode(p, p, p, p, p, p, 48, 3, 64, 512, p, None) == 1           # 16 heads per KV head
+    assert lib.aq_attn_decode(p, p, p, p, p, p, 32, 4, 64, 8192, p, None) == 6          # scores exceed LDS
+    assert lib.aq_attn_decode(p, p, p, None, p, p, 32, 8, 64, 512, p, None) == 5
+    # lm_head: 128256 rows need 4 * 1024 argmax candidates; the position pointer is required
+    assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 128256, 2048, 32, p, 1000, p, p, None, 0, 1, None) == 6
+    assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 1000, 2048, 32, p, 4096, p, None, None, 0, 1, None) == 5
+    assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 1000, 2048, 32, p + 4, 4096, p, p, None, 0, 1, None) == 3
+
+
+def test_decode_ops_registered():
+    import torch
+    from aq import ops  # noqa: F401
+    for name in ("rmsnorm_gemv_q4", "rmsnorm_gate_up_q4", "embed_f16", "attn_decode", "head_argmax_q4"):
+        assert hasattr(torch.ops.aq, name)
