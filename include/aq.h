@@ -203,6 +203,26 @@ int aq_attn_decode(const float* qkv, const float* cos_tab, const float* sin_tab,
                    const int32_t* pos, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_pos, float* out,
                    void* stream);
 
+/* Split attention (flash decoding), the decode step's form of aq_attn_decode: the positions of each KV head are cut
+ * into `splits` spans of ceil(max_pos / splits) rounded up to 64, one workgroup each (kv_heads * splits workgroups
+ * instead of kv_heads), and each writes the partial softmax state of its span for every query head h:
+ *   parts: o [heads][splits][64] (sum over the span of e^(s - m) v), then (m, l) [heads][splits][2] (the span's max
+ *   score and sum of e^(s - m)); a span past the position holds m = -inf, l = 0, o = 0.
+ * RoPE and the cache append are as in aq_attn_decode. aq_attn_out_q4 combines the spans. 1 <= splits <=
+ * AQ_ATTN_MAX_SPLITS; (heads / kv_heads) * span floats of LDS <= 64 KB. No counterpart in the reference (its attention
+ * is one workgroup per head, llama/kernels/attention.mojo:19-66); same result to fp32 rounding. */
+#define AQ_ATTN_MAX_SPLITS 8
+int aq_attn_decode_split(const float* qkv, const float* cos_tab, const float* sin_tab, uint16_t* k_cache,
+                         uint16_t* v_cache, const int32_t* pos, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                         int32_t max_pos, int32_t splits, float* parts, void* stream);
+
+/* y += W . att, where att [k = heads * 64] is combined from the split-attention states while x is staged:
+ * att[h, d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c. Otherwise aq_gemv_q4 (add = 1,
+ * tokens = 1). Replaces: gemv_add_q4 of the attention output (llama/model.mojo:150, llama/kernels/gemv_add_q4.mojo:
+ * 13-30), with the split combine folded in. */
+int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, int32_t splits, float* y, int64_t n,
+                   int64_t k, int32_t group, void* stream);
+
 /* Final norm, lm_head and greedy argmax: logits = W . rmsnorm(x) (norm_w NULL: x as given), then *token = the first
  * index of the largest logit, hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance.
  * cand: device scratch of AQ_HEAD_CANDIDATES argmax keys (8-byte aligned). Replaces: Llama.head

@@ -46,6 +46,8 @@ SIGNATURES: dict[str, list] = {
     "aq_rmsnorm_gate_up_q4": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _i32, _i32, _p],
     "aq_embed_f16": [_p, _i64, _i64, _p, _p, _p],
     "aq_attn_decode": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _p, _p],
+    "aq_attn_decode_split": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p],
+    "aq_attn_out_q4": [_p, _p, _p, _i32, _p, _i64, _i64, _i32, _p],
     "aq_head_argmax_q4": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _i32, _i32,
                           _p],
     "aq_quantize_q4": [_p, _i32, _i64, _i64, _i32, _p, _p],

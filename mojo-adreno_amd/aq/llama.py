@@ -7,8 +7,9 @@ llama/llama.mojo:50-80 (one token at a time; its batched ``prefill`` is the GEMM
 
     embed(token)                                   aq_embed_f16
     per layer:  qkv = Wqkv . rmsnorm(x)           aq_rmsnorm_gemv_q4      (rmsnorm fused into the x staging)
-                att = attention(rope(qkv), cache)  aq_attn_decode          (RoPE + cache append + softmax . V)
-                x += Wo . att                      aq_gemv_q4 (add)
+                att = attention(rope(qkv), cache)  aq_attn_decode_split    (RoPE + cache append + softmax . V over
+                                                                            spans of positions: partial states)
+                x += Wo . att                      aq_attn_out_q4          (the spans combined on staging)
                 a = silu(Wg . rmsnorm(x)) * (Wu . rmsnorm(x))   aq_rmsnorm_gate_up_q4
                 x += Wdown . a                     aq_gemv_q4 (add)
     logits = Wlm . rmsnorm(x); token = argmax      aq_head_argmax_q4        (argmax on the device)
@@ -154,7 +155,9 @@ class LlamaDecoder:
         f32 = dict(dtype=torch.float32, device=dev)
         self.x = torch.zeros(cfg.dim, **f32)
         self.qkv = torch.zeros(cfg.qkv, **f32)
-        self.att = torch.zeros(cfg.heads * cfg.head_dim, **f32)
+        # split attention: spans of >= 64 positions, at most 8 (the states are combined by the o projection)
+        self.splits = max(1, min(ops.ATTN_MAX_SPLITS, cfg.max_pos // 64))
+        self.parts = torch.zeros(ops.attn_parts_numel(cfg.heads, self.splits), **f32)
         self.act = torch.zeros(cfg.ffn, **f32)
         self.logits = torch.zeros(cfg.vocab, **f32)
         shape = (cfg.kv_heads, cfg.max_pos, cfg.head_dim)
@@ -174,9 +177,9 @@ class LlamaDecoder:
         a.embed_f16(w.embed, self.token, self.x)
         for i, lw in enumerate(w.layers):
             a.rmsnorm_gemv_q4(*lw["wqkv"], self.x, lw["attn_norm"], cfg.eps, self.qkv, cfg.group)
-            a.attn_decode(self.qkv, self.cos, self.sin, self.kc[i], self.vc[i], self.pos, cfg.heads, cfg.kv_heads,
-                          self.att)
-            a.gemv_q4(*lw["wo"], self.att, self.x, cfg.group, True)
+            a.attn_decode_split(self.qkv, self.cos, self.sin, self.kc[i], self.vc[i], self.pos, cfg.heads,
+                                cfg.kv_heads, self.splits, self.parts)
+            a.attn_out_q4(*lw["wo"], self.parts, self.splits, self.x, cfg.group)
             a.rmsnorm_gate_up_q4(*lw["wgu"], self.x, lw["mlp_norm"], cfg.eps, self.act, cfg.group)
             a.gemv_q4(*lw["wdown"], self.act, self.x, cfg.group, True)
         a.head_argmax_q4(*w.lm, self.x, w.final_norm, cfg.eps, self.logits, cfg.group, self.cand, self.token, self.pos,

@@ -398,6 +398,12 @@ for _name, _fn in (("moe_route", _moe_route_impl), ("moe_group", _moe_group_impl
 # ---- Llama decode step: fused norms, embedding, attention, lm_head + argmax -----------------------------------------
 
 HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax keys of the lm_head launch
+ATTN_MAX_SPLITS = 8     # AQ_ATTN_MAX_SPLITS
+
+
+def attn_parts_numel(heads: int, splits: int) -> int:
+    """Floats of the split-attention state buffer: o [heads][splits][64], then (m, l) [heads][splits][2]."""
+    return heads * splits * 66
 
 _LIB.define("rmsnorm_gemv_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) y, int group) -> ()")
 _LIB.define("rmsnorm_gate_up_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) a, int group)"
@@ -405,6 +411,9 @@ _LIB.define("rmsnorm_gate_up_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, f
 _LIB.define("embed_f16(Tensor table, Tensor token, Tensor(a!) x) -> ()")
 _LIB.define("attn_decode(Tensor qkv, Tensor cos, Tensor sin, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor pos, "
             "int heads, int kv_heads, Tensor(c!) out) -> ()")
+_LIB.define("attn_decode_split(Tensor qkv, Tensor cos, Tensor sin, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+            "Tensor pos, int heads, int kv_heads, int splits, Tensor(c!) parts) -> ()")
+_LIB.define("attn_out_q4(Tensor wq, Tensor ws, Tensor parts, int splits, Tensor(a!) y, int group) -> ()")
 _LIB.define("head_argmax_q4(Tensor wq, Tensor ws, Tensor x, Tensor norm_w, float eps, Tensor(a!) logits, int group, "
             "Tensor(b!) cand, Tensor(c!) token, Tensor(d!) pos, Tensor(e!) hist, int advance) -> ()")
 
@@ -466,6 +475,32 @@ def _attn_decode_impl(qkv, cos, sin, k_cache, v_cache, pos, heads, kv_heads, out
               kv_heads, 64, max_pos, _ptr(out), _stream(qkv))
 
 
+def _attn_decode_split_impl(qkv, cos, sin, k_cache, v_cache, pos, heads, kv_heads, splits, parts):
+    _dev(qkv, cos, sin, k_cache, v_cache, pos, parts)
+    _check(qkv.dtype == torch.float32 and parts.dtype == torch.float32, "qkv and parts must be float32")
+    _check(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin must be float32")
+    _f16bits(k_cache, "k_cache")
+    _f16bits(v_cache, "v_cache")
+    _check(pos.dtype == torch.int32 and pos.numel() >= 1, "pos must be int32 on the device")
+    _check(k_cache.dim() == 3 and k_cache.shape[0] == kv_heads and k_cache.shape[2] == 64, "k_cache [kv_heads, P, 64]")
+    max_pos = k_cache.shape[1]
+    _check(tuple(v_cache.shape) == tuple(k_cache.shape), "v_cache must match k_cache")
+    _check(qkv.numel() == (heads + 2 * kv_heads) * 64, "qkv size")
+    _check(cos.numel() == max_pos * 32 and sin.numel() == max_pos * 32, "cos/sin must be [max_pos, 32]")
+    _check(parts.numel() >= attn_parts_numel(heads, splits), "parts too small")
+    _lib.call("aq_attn_decode_split", _ptr(qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(pos), heads,
+              kv_heads, 64, max_pos, splits, _ptr(parts), _stream(qkv))
+
+
+def _attn_out_q4_impl(wq, ws, parts, splits, y, group):
+    _dev(wq, ws, parts, y)
+    n, k = _q4_shape(wq, ws, group)
+    _check(parts.dtype == torch.float32 and y.dtype == torch.float32, "parts and y must be float32")
+    _check(k % 64 == 0 and parts.numel() >= attn_parts_numel(k // 64, splits), "parts too small for K / 64 heads")
+    _check(y.numel() == n, "y must be [N]")
+    _lib.call("aq_attn_out_q4", _ptr(wq), _ptr(ws), _ptr(parts), splits, _ptr(y), n, k, group, _stream(y))
+
+
 def _head_argmax_q4_impl(wq, ws, x, norm_w, eps, logits, group, cand, token, pos, hist, advance):
     _dev(wq, ws, x, logits, cand, token, pos)
     vocab, k = _q4_shape(wq, ws, group)
@@ -490,5 +525,6 @@ def _head_argmax_q4_impl(wq, ws, x, norm_w, eps, logits, group, cand, token, pos
 
 for _name, _fn in (("rmsnorm_gemv_q4", _rmsnorm_gemv_q4_impl), ("rmsnorm_gate_up_q4", _rmsnorm_gate_up_q4_impl),
                    ("embed_f16", _embed_f16_impl), ("attn_decode", _attn_decode_impl),
+                   ("attn_decode_split", _attn_decode_split_impl), ("attn_out_q4", _attn_out_q4_impl),
                    ("head_argmax_q4", _head_argmax_q4_impl)):
     _LIB.impl(_name, _fn, "CUDA")

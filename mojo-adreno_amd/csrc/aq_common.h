@@ -10,6 +10,10 @@ namespace aq {
 
 constexpr int kWave = 64;
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 // Cross-lane moves by DPP (a VALU operand modifier: no LDS round trip). CTRL: quad_perm 0x00-0xFF, row_mirror 0x140,
 // row_half_mirror 0x141, row_ror:n 0x120 + n, row_bcast:15 0x142, row_bcast:31 0x143 (rows are 16 lanes).
 template <int CTRL, int ROW_MASK = 0xF>

@@ -5,10 +5,6 @@
 
 namespace aq {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-
 constexpr int kSuper = 128;  // k per super-step
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {

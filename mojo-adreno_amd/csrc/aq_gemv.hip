@@ -28,10 +28,14 @@ struct MoeArgs {
 // Decode-step fusions. norm != NULL: every token's x is RMS-normalised on staging, x * (1 / sqrt(mean(x^2) + eps))
 // * norm[k] (fp16 weights), so no separate norm kernel runs before the product. cand != NULL (kStore, one token):
 // each wave also leaves the largest output it wrote and its row, as an argmax key (cand[block * 4 + wave]).
+// parts != NULL (one token): x is the attention output combined from `splits` partial softmax states (the layout of
+// aq_attn_decode_split): x[h * 64 + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
 struct Fuse {
   const uint16_t* norm;
   float eps;
   uint64_t* cand;
+  const float* parts;
+  int splits;
 };
 
 // Argmax key: larger for a larger value and, among equal values, for a smaller index, so the maximum key names the
@@ -63,7 +67,13 @@ template <bool G32, int R, int T, int MODE, int D>
 __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
                                                  int k, int group, int f, int tokens, MoeArgs moe, Fuse fz) {
-  // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots):
+  // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots). G32 (not kMoeDown):
+  //   xh[t][j][c]   uint4: x[t, 32c + 8j + (0, 4)], (1, 5), (2, 6), (3, 7) as fp16 pairs (the high parts) (T * 4 planes)
+  //   xl[t][j][c]   uint4: the same pairs of x - high part (the low parts)                             (T * 4 planes)
+  //   xb[t][c]      float4: (bias, 1 / f, -, -): f = the chunk's power-of-two scale (x is staged as f * x, its
+  //                 largest magnitude in [2^9, 2^10), so the low parts stay normal fp16, which v_dot2 needs) and
+  //                 bias = sum over the chunk of 1032 f x_k (k % 8 even) or 72 f x_k (odd), the magic values' offset
+  // otherwise:
   //   xs4[t][p][c]  float4 p = 2j + h holds x[t, 32c + 8j + 4h .. + 3]  (T * 8 planes of nch float4)
   //   xsum[t][j][c] sum of x[t, 32c + 8j .. + 7]                        (T * 4 planes of nch floats)
   extern __shared__ float4 lds4[];
@@ -72,6 +82,11 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   const int nch = k >> 5;
   float4* xs4 = lds4;
   float* xsum = reinterpret_cast<float*>(lds4 + T * 8 * nch);
+  uint4* xh = reinterpret_cast<uint4*>(lds4);
+  uint4* xl = xh + T * 4 * nch;
+  float4* xb = lds4 + T * 8 * nch;
+  // fp16-pair products (v_dot2_f32_f16) for the G32 modes but kMoeDown
+  constexpr bool kHalfX = G32 && MODE != kMoeDown;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int gpr = k / group;
@@ -100,27 +115,46 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       sc[r] = ok ? ws[(size_t)rows[r] * gpr + ((c * 32) >> gsh)] : (uint16_t)0;
     }
   };
+  // One chunk: each word's 8 codes become 4 fp16 pairs holding the exact values 1024 + n (bits 0-3, 16-19 of the
+  // word, and of the word >> 8) or 64 + n (bits 4-7, 20-23), n = stored nibble ^ 8 = q + 8, one v_bitop3 each:
+  // ((w ^ 0x8..8) & mask) | magic. Their dot products with the fp16 high and low parts of x (v_dot2_f32_f16: exact
+  // products, fp32 sums) minus the staged bias sum_k (1032 or 72) x_k leave sum_k q_k x_k.
   auto use_chunk = [&](int c, const uint4 (&w)[R], const uint16_t (&sc)[R], float (&acc)[R][T]) {
+    half2v pr[R][4][4];  // [row][word][pair]
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const float* s4 = xsum + t * 4 * nch + c;
-      const float xs32 = (s4[0] + s4[nch]) + (s4[2 * nch] + s4[3 * nch]);
-      float part[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[r] = -8.0f * xs32;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float xv[8];
-        *reinterpret_cast<float4*>(xv) = xs4[(t * 8 + 2 * j) * nch + c];
-        *reinterpret_cast<float4*>(xv + 4) = xs4[(t * 8 + 2 * j + 1) * nch + c];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
-          part[r] += dot8_biased(wj, xv);
-        }
+        const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
+        const uint32_t w8 = wj >> 8;
+        pr[r][j][0] = __builtin_bit_cast(half2v, ((wj ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
+        pr[r][j][1] = __builtin_bit_cast(half2v, ((wj ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
+        pr[r][j][2] = __builtin_bit_cast(half2v, ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
+        pr[r][j][3] = __builtin_bit_cast(half2v, ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
       }
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]), acc[r][t]);
+    for (int t = 0; t < T; ++t) {
+      const float4 bw = xb[t * nch + c];
+      float part[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[r] = -bw.x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 hi = xh[(t * 4 + j) * nch + c], lo = xl[(t * 4 + j) * nch + c];
+        const half2v h4[4] = {__builtin_bit_cast(half2v, hi.x), __builtin_bit_cast(half2v, hi.y),
+                              __builtin_bit_cast(half2v, hi.z), __builtin_bit_cast(half2v, hi.w)};
+        const half2v l4[4] = {__builtin_bit_cast(half2v, lo.x), __builtin_bit_cast(half2v, lo.y),
+                              __builtin_bit_cast(half2v, lo.z), __builtin_bit_cast(half2v, lo.w)};
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], h4[q], part[r], false);
+            part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], l4[q], part[r], false);
+          }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]) * bw.y, acc[r][t]);
     }
   };
 
@@ -179,7 +213,37 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       const int c = wi >> 2;
       const int j = wi & 3;
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      if (t < tokens) {
+      if (fz.parts) {  // workgroup-uniform; one token: dimensions 8 (wi % 8) .. + 7 of head wi / 8
+        const int h = wi >> 3, d0 = (wi & 7) * 8, S = fz.splits;
+        const float* po = fz.parts + (size_t)h * S * 64 + d0;
+        const float* pml = fz.parts + (size_t)(k / 64) * S * 64 + (size_t)h * S * 2;
+        float mv[AQ_ATTN_MAX_SPLITS], lv[AQ_ATTN_MAX_SPLITS];
+        float4 oa[AQ_ATTN_MAX_SPLITS], ob[AQ_ATTN_MAX_SPLITS];
+#pragma unroll
+        for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {  // all requests first
+          const int ci = cc < S ? cc : 0;
+          mv[cc] = pml[2 * ci];
+          lv[cc] = pml[2 * ci + 1];
+          oa[cc] = *reinterpret_cast<const float4*>(po + ci * 64);
+          ob[cc] = *reinterpret_cast<const float4*>(po + ci * 64 + 4);
+        }
+        float mx = mv[0];
+#pragma unroll
+        for (int cc = 1; cc < AQ_ATTN_MAX_SPLITS; ++cc) mx = cc < S ? fmaxf(mx, mv[cc]) : mx;
+        float den = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
+          const float w = cc < S ? expf(mv[cc] - mx) : 0.f;  // a split with no positions has m = -inf: weight 0
+          den = fmaf(w, lv[cc], den);
+          a.x = fmaf(w, oa[cc].x, a.x); a.y = fmaf(w, oa[cc].y, a.y);
+          a.z = fmaf(w, oa[cc].z, a.z); a.w = fmaf(w, oa[cc].w, a.w);
+          b.x = fmaf(w, ob[cc].x, b.x); b.y = fmaf(w, ob[cc].y, b.y);
+          b.z = fmaf(w, ob[cc].z, b.z); b.w = fmaf(w, ob[cc].w, b.w);
+        }
+        const float r = 1.0f / den;
+        a.x *= r; a.y *= r; a.z *= r; a.w *= r;
+        b.x *= r; b.y *= r; b.z *= r; b.w *= r;
+      } else if (t < tokens) {
         const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
         a = src[0];
         b = src[1];
@@ -197,9 +261,37 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
           b.w *= half_bits_to_float(wn.w >> 16);
         }
       }
-      xs4[(t * 8 + 2 * j) * nch + c] = a;
-      xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
-      xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+      if constexpr (kHalfX) {  // pairs (0, 4), (1, 5), (2, 6), (3, 7), split into fp16 high and low parts
+        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        // the chunk's scale: the 4 threads of a quad hold its 4 words (whole quads run each iteration: K % 32 == 0)
+        uint32_t e = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
+        e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
+        e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
+        const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
+        const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] *= f;
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
+          const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
+          hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
+        bias += dpp<0xB1>(0.f, bias);
+        bias += dpp<0x4E>(0.f, bias);
+        if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
+      } else {
+        xs4[(t * 8 + 2 * j) * nch + c] = a;
+        xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
+        xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+      }
     }
   }
   if (fz.norm) {
@@ -466,7 +558,7 @@ static int launch_g(const uint32_t* wq, const uint16_t* ws, const float* x, floa
 template <int MODE>
 static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int64_t n_out, int64_t k,
                       int32_t group, int64_t f, int32_t tokens, const MoeArgs& moe, void* stream,
-                      const Fuse& fz = Fuse{nullptr, 0.f, nullptr}) {
+                      const Fuse& fz = Fuse{nullptr, 0.f, nullptr, nullptr, 0}) {
   if (!wq || !ws || !x || !y) return AQ_ERR_NULL;
   if (fz.norm && !aligned(fz.norm, 16)) return AQ_ERR_ALIGN;
   if (n_out <= 0 || k <= 0 || tokens < 1 || tokens > 8) return AQ_ERR_SHAPE;
@@ -552,7 +644,7 @@ extern "C" int aq_rmsnorm_gemv_q4(const uint32_t* wq, const uint16_t* ws, const 
                                   void* stream) {
   if (!norm_w) return AQ_ERR_NULL;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
-  return aq::gemv_entry<aq::kStore>(wq, ws, x, y, n, k, group, 0, tokens, none, stream, aq::Fuse{norm_w, eps, nullptr});
+  return aq::gemv_entry<aq::kStore>(wq, ws, x, y, n, k, group, 0, tokens, none, stream, aq::Fuse{norm_w, eps, nullptr, nullptr, 0});
 }
 
 extern "C" int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
@@ -561,7 +653,7 @@ extern "C" int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, con
   if (!norm_w) return AQ_ERR_NULL;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
   return aq::gemv_entry<aq::kGateUp>(wq, ws, x, a, f, k, group, f, tokens, none, stream,
-                                     aq::Fuse{norm_w, eps, nullptr});
+                                     aq::Fuse{norm_w, eps, nullptr, nullptr, 0});
 }
 
 extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
@@ -575,9 +667,20 @@ extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const f
   if (!aq::aligned(cand, 8)) return AQ_ERR_ALIGN;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
   const int st = aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream,
-                                            aq::Fuse{norm_w, eps, cand});
+                                            aq::Fuse{norm_w, eps, cand, nullptr, 0});
   if (st != AQ_OK) return st;
   hipLaunchKernelGGL(aq::k_argmax_step, dim3(1), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), cand, ncand,
                      token, pos, hist, hist_cap, advance);
   return aq::launch_status();
+}
+
+extern "C" int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, int32_t splits, float* y,
+                              int64_t n, int64_t k, int32_t group, void* stream) {
+  if (!parts) return AQ_ERR_NULL;
+  if (splits < 1 || splits > AQ_ATTN_MAX_SPLITS || k % 64) return AQ_ERR_SHAPE;
+  if (!aq::aligned(parts, 16)) return AQ_ERR_ALIGN;
+  const aq::MoeArgs none{nullptr, nullptr, 0, 0};
+  // x is not read (the partial states stand for it); parts is passed as x for the pointer checks
+  return aq::gemv_entry<aq::kAdd>(wq, ws, parts, y, n, k, group, 0, 1, none, stream,
+                                  aq::Fuse{nullptr, 0.f, nullptr, parts, splits});
 }

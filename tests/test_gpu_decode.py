@@ -176,14 +176,27 @@ def _decoder(cfg, seed, dev):
                          ids=["small", "llama1b-width-2-layers"])
 def test_decode_steps_vs_oracle(dev, cfg_kw):
     """Token-by-token forward steps: logits within rel 1e-3 of the float64 oracle (same fp16 cache rounding) at every
-    step, and the device argmax is the first maximum of those logits."""
+    step, and the device argmax is the first maximum of those logits.
+
+    A cached value that sits on an fp16 rounding boundary can round either way between the GPU's fp32 and the
+    oracle's float64 arithmetic, and a small random model can amplify that: the bar is widened by twice the model's
+    own sensitivity to its cache's rounding (the oracle with an fp16 cache against the oracle with a float64 one),
+    which is ~1e-5 at Llama-1B width and up to a few 1e-3 for the 512-wide model."""
     cfg = _small_cfg(**cfg_kw)
     dec, oracle = _decoder(cfg, 21, dev)
+    from aq import synth
+    from aq.llama import rope_tables
+    arrays = synth.llama_arrays(cfg, 21)
+    arrays["embed"] = (arrays["embed"].astype(np.float32) * 0.1).astype(np.float16)
+    exact = orc.LlamaDecodeOracle(arrays, cfg, *rope_tables(cfg), kv_dtype=None)
     tokens = [1, 500, 999, 2, 2, 300, 17, 64, 0, 777][:10]
     for pos, t in enumerate(tokens):
         lg = to_np(dec.forward(t, pos))
         ref = oracle.step(t, pos)
-        assert rel_inf(lg, ref) < TOL, pos
+        sensitivity = rel_inf(ref, exact.step(t, pos))
+        assert rel_inf(lg, ref) < TOL + 2 * sensitivity, (pos, sensitivity)
+        if cfg.dim == 2048:
+            assert rel_inf(lg, ref) < TOL, pos
         assert int(dec.token.item()) == orc.argmax_first(lg)
         assert int(dec.pos.item()) == pos + 1
 
@@ -235,3 +248,36 @@ def test_graph_replay_is_bitwise_eager(dev):
         assert torch.equal(b.logits, logits_a[i])
     assert int(b.pos.item()) == 6
     np.testing.assert_array_equal(to_np(b.hist[:6]), np.array(toks_a, np.int32))
+
+
+@pytest.mark.parametrize("heads,kv,max_pos,pos,splits", [
+    (32, 8, 512, 511, 8), (32, 8, 512, 0, 8), (32, 8, 512, 63, 8), (32, 8, 512, 64, 8), (32, 8, 512, 300, 3),
+    (4, 2, 64, 63, 1), (16, 2, 1024, 777, 8), (8, 1, 200, 150, 7), (8, 8, 4096, 4000, 8),
+])
+def test_split_attention_and_combined_output_projection(dev, heads, kv, max_pos, pos, splits):
+    """aq_attn_decode_split writes the cache row as aq_attn_decode does, and aq_attn_out_q4 (the spans combined while
+    staging x) equals y + Wo . attention(q, cache) of the oracle."""
+    import torch
+    from aq import ops
+    rng = np.random.default_rng(heads + kv + max_pos + pos + splits)
+    cos, sin = _rope_np(max_pos)
+    qkv = (rng.standard_normal((heads + 2 * kv) * 64) * 2).astype(np.float32)
+    kc0 = rng.standard_normal((kv, max_pos, 64)).astype(np.float16)
+    vc0 = rng.standard_normal((kv, max_pos, 64)).astype(np.float16)
+    kc, vc = to_dev(kc0, dev), to_dev(vc0, dev)
+    parts = torch.full((ops.attn_parts_numel(heads, splits),), float("nan"), dtype=torch.float32, device=dev)
+    torch.ops.aq.attn_decode_split(to_dev(qkv, dev), to_dev(cos, dev), to_dev(sin, dev), kc, vc,
+                                   torch.tensor([pos], dtype=torch.int32, device=dev), heads, kv, splits, parts)
+    kg, vg = to_np(kc).view(np.float16), to_np(vc).view(np.float16)
+    np.testing.assert_array_equal(vg[:, pos], qkv[(heads + kv) * 64:].reshape(kv, 64).astype(np.float16))
+    keep = np.ones(max_pos, bool)
+    keep[pos] = False
+    np.testing.assert_array_equal(kg[:, keep], kc0[:, keep])
+    q = orc.rope(qkv[:heads * 64].reshape(heads, 64), cos[pos], sin[pos])
+    att = orc.attention_decode(q, kg.astype(np.float64), vg.astype(np.float64), pos + 1).reshape(-1)
+    n = 700
+    wq, ws = _int4(rng, n, heads * 64)
+    y0 = rng.standard_normal(n).astype(np.float32)
+    y = to_dev(y0, dev)
+    torch.ops.aq.attn_out_q4(to_dev(wq, dev), to_dev(ws, dev), parts, splits, y, 32)
+    assert rel_inf(to_np(y), orc.gemv_q4(wq, ws, att, 32, y0=y0)) < TOL

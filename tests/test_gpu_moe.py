@@ -199,7 +199,7 @@ def test_invalid_ids_are_inert(dev):
         ex = ids[j]
         h = orc.gemv_q4(gu_q[ex * 2 * f:(ex + 1) * 2 * f], gu_s[ex * 2 * f:(ex + 1) * 2 * f], x, g)
         act = orc.silu(h[:f]) * h[f:]
-        np.testing.assert_allclose(an[j], act, rtol=1e-4, atol=1e-5)
+        assert rel_inf(an[j], act) < 1e-4
         ref += wts[j] * orc.gemv_q4(dn_q[ex * d:(ex + 1) * d], dn_s[ex * d:(ex + 1) * d], an[j], g)
     assert rel_inf(to_np(y), ref) < 1e-4
 
