@@ -63,7 +63,10 @@ __device__ __forceinline__ int gemv_row(int base, int r, int n_out, int f, const
 
 // G32: the group size is a power of two >= 32 (one scale per 32-weight chunk). Otherwise every word looks up its own.
 // D: register sets of the chunk pipeline (dense G32 modes), chosen at launch from the chunks a wave has.
-template <bool G32, int R, int T, int MODE, int D>
+// XR: one token, K <= 256 * XR * 8, x given (not split-attention states): each thread requests its XR words of x
+// into registers before the weights, so their staging overlaps the weights' arrival (vector memory completes in
+// order: x requested after the weights would wait for them). 0: x is loaded while it is staged.
+template <bool G32, int R, int T, int MODE, int D, int XR>
 __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
                                                  int k, int group, int f, int tokens, MoeArgs moe, Fuse fz) {
@@ -188,6 +191,28 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     }
     if (ib < n_out && ++ic == cpl) ic = 0, ib += stride;
   };
+  constexpr int kXi = XR > 0 ? XR : 1;
+  float4 xra[kXi], xrb[kXi];
+  uint4 xrn[kXi];
+  if constexpr (XR > 0) {
+    // the norm weights first: a wait for x, which comes after them, then covers them, whether or not they exist
+    if (fz.norm) {
+      const __amdgpu_buffer_rsrc_t n_rsrc = make_rsrc(fz.norm, (uint32_t)k * 2);
+#pragma unroll
+      for (int i = 0; i < kXi; ++i) {
+        const uint32_t wi = threadIdx.x + 256 * i;
+        xrn[i] = buf_load16(n_rsrc, wi < (uint32_t)kw ? wi * 16 : kOOB);
+      }
+    }
+    const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(x, (uint32_t)k * 4);
+#pragma unroll
+    for (int i = 0; i < kXi; ++i) {
+      const uint32_t wi = threadIdx.x + 256 * i;
+      const bool ok = wi < (uint32_t)kw;
+      xra[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 : kOOB));
+      xrb[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 + 16 : kOOB));
+    }
+  }
   if constexpr (kDeep) {
 #pragma unroll
     for (int d = 0; d < D; ++d) issue_next(wd[d], sd[d], sh[d]);
@@ -207,90 +232,103 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   // scaled by 1 / sqrt(mean(x^2) + eps) (a per-token scalar), which is the RMSNorm'd product.
   float ss[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    ss[t] = 0.f;
-    for (int wi = threadIdx.x; wi < kw; wi += 256) {
-      const int c = wi >> 2;
-      const int j = wi & 3;
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      if (fz.parts) {  // workgroup-uniform; one token: dimensions 8 (wi % 8) .. + 7 of head wi / 8
-        const int h = wi >> 3, d0 = (wi & 7) * 8, S = fz.splits;
-        const float* po = fz.parts + (size_t)h * S * 64 + d0;
-        const float* pml = fz.parts + (size_t)(k / 64) * S * 64 + (size_t)h * S * 2;
-        float mv[AQ_ATTN_MAX_SPLITS], lv[AQ_ATTN_MAX_SPLITS];
-        float4 oa[AQ_ATTN_MAX_SPLITS], ob[AQ_ATTN_MAX_SPLITS];
+  for (int t = 0; t < T; ++t) ss[t] = 0.f;
+  // word wi (8 values) of token t: norm, then the LDS layouts above
+  auto stage = [&](int t, int wi, float4 a, float4 b, const uint4 wn) {
+    const int c = wi >> 2;
+    const int j = wi & 3;
+    if (fz.norm) {  // workgroup-uniform
+      ss[t] += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) + ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+      a.x *= half_bits_to_float(wn.x & 0xFFFF);
+      a.y *= half_bits_to_float(wn.x >> 16);
+      a.z *= half_bits_to_float(wn.y & 0xFFFF);
+      a.w *= half_bits_to_float(wn.y >> 16);
+      b.x *= half_bits_to_float(wn.z & 0xFFFF);
+      b.y *= half_bits_to_float(wn.z >> 16);
+      b.z *= half_bits_to_float(wn.w & 0xFFFF);
+      b.w *= half_bits_to_float(wn.w >> 16);
+    }
+    if constexpr (kHalfX) {  // pairs (0, 4), (1, 5), (2, 6), (3, 7), split into fp16 high and low parts
+      float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      // the chunk's scale: the 4 threads of a quad hold its 4 words (whole quads run each iteration: K % 32 == 0)
+      uint32_t e = 0;
 #pragma unroll
-        for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {  // all requests first
-          const int ci = cc < S ? cc : 0;
-          mv[cc] = pml[2 * ci];
-          lv[cc] = pml[2 * ci + 1];
-          oa[cc] = *reinterpret_cast<const float4*>(po + ci * 64);
-          ob[cc] = *reinterpret_cast<const float4*>(po + ci * 64 + 4);
-        }
-        float mx = mv[0];
+      for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
+      e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
+      e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
+      const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
+      const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
 #pragma unroll
-        for (int cc = 1; cc < AQ_ATTN_MAX_SPLITS; ++cc) mx = cc < S ? fmaxf(mx, mv[cc]) : mx;
-        float den = 0.f;
+      for (int q = 0; q < 8; ++q) v[q] *= f;
+      uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
-          const float w = cc < S ? expf(mv[cc] - mx) : 0.f;  // a split with no positions has m = -inf: weight 0
-          den = fmaf(w, lv[cc], den);
-          a.x = fmaf(w, oa[cc].x, a.x); a.y = fmaf(w, oa[cc].y, a.y);
-          a.z = fmaf(w, oa[cc].z, a.z); a.w = fmaf(w, oa[cc].w, a.w);
-          b.x = fmaf(w, ob[cc].x, b.x); b.y = fmaf(w, ob[cc].y, b.y);
-          b.z = fmaf(w, ob[cc].z, b.z); b.w = fmaf(w, ob[cc].w, b.w);
-        }
-        const float r = 1.0f / den;
-        a.x *= r; a.y *= r; a.z *= r; a.w *= r;
-        b.x *= r; b.y *= r; b.z *= r; b.w *= r;
-      } else if (t < tokens) {
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
-        a = src[0];
-        b = src[1];
-        if (fz.norm) {  // workgroup-uniform
-          ss[t] += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
-                   ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
-          const uint4 wn = *reinterpret_cast<const uint4*>(fz.norm + wi * 8);
-          a.x *= half_bits_to_float(wn.x & 0xFFFF);
-          a.y *= half_bits_to_float(wn.x >> 16);
-          a.z *= half_bits_to_float(wn.y & 0xFFFF);
-          a.w *= half_bits_to_float(wn.y >> 16);
-          b.x *= half_bits_to_float(wn.z & 0xFFFF);
-          b.y *= half_bits_to_float(wn.z >> 16);
-          b.z *= half_bits_to_float(wn.w & 0xFFFF);
-          b.w *= half_bits_to_float(wn.w >> 16);
-        }
+      for (int q = 0; q < 4; ++q) {
+        const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
+        const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
+        hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
       }
-      if constexpr (kHalfX) {  // pairs (0, 4), (1, 5), (2, 6), (3, 7), split into fp16 high and low parts
-        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        // the chunk's scale: the 4 threads of a quad hold its 4 words (whole quads run each iteration: K % 32 == 0)
-        uint32_t e = 0;
+      xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
+      bias += dpp<0xB1>(0.f, bias);
+      bias += dpp<0x4E>(0.f, bias);
+      if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
+    } else {
+      xs4[(t * 8 + 2 * j) * nch + c] = a;
+      xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
+      xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    }
+  };
+  if constexpr (XR > 0) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
-        e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
-        e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
-        const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
-        const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
+    for (int i = 0; i < kXi; ++i) {
+      const int wi = threadIdx.x + 256 * i;
+      if (wi < kw) stage(0, wi, xra[i], xrb[i], xrn[i]);
+    }
+  } else {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] *= f;
-        uint32_t hw[4], lw[4];
+    for (int t = 0; t < T; ++t) {
+      for (int wi = threadIdx.x; wi < kw; wi += 256) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        uint4 wn = make_uint4(0u, 0u, 0u, 0u);
+        if (fz.parts) {  // workgroup-uniform; one token: dimensions 8 (wi % 8) .. + 7 of head wi / 8
+          const int h = wi >> 3, d0 = (wi & 7) * 8, S = fz.splits;
+          const float* po = fz.parts + (size_t)h * S * 64 + d0;
+          const float* pml = fz.parts + (size_t)(k / 64) * S * 64 + (size_t)h * S * 2;
+          float mv[AQ_ATTN_MAX_SPLITS], lv[AQ_ATTN_MAX_SPLITS];
+          float4 oa[AQ_ATTN_MAX_SPLITS], ob[AQ_ATTN_MAX_SPLITS];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
-          const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
-          hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-          lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+          for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {  // all requests first
+            const int ci = cc < S ? cc : 0;
+            mv[cc] = pml[2 * ci];
+            lv[cc] = pml[2 * ci + 1];
+            oa[cc] = *reinterpret_cast<const float4*>(po + ci * 64);
+            ob[cc] = *reinterpret_cast<const float4*>(po + ci * 64 + 4);
+          }
+          float mx = mv[0];
+#pragma unroll
+          for (int cc = 1; cc < AQ_ATTN_MAX_SPLITS; ++cc) mx = cc < S ? fmaxf(mx, mv[cc]) : mx;
+          float den = 0.f;
+#pragma unroll
+          for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
+            const float w = cc < S ? expf(mv[cc] - mx) : 0.f;  // a split with no positions has m = -inf: weight 0
+            den = fmaf(w, lv[cc], den);
+            a.x = fmaf(w, oa[cc].x, a.x); a.y = fmaf(w, oa[cc].y, a.y);
+            a.z = fmaf(w, oa[cc].z, a.z); a.w = fmaf(w, oa[cc].w, a.w);
+            b.x = fmaf(w, ob[cc].x, b.x); b.y = fmaf(w, ob[cc].y, b.y);
+            b.z = fmaf(w, ob[cc].z, b.z); b.w = fmaf(w, ob[cc].w, b.w);
+          }
+          const float r = 1.0f / den;
+          a.x *= r; a.y *= r; a.z *= r; a.w *= r;
+          b.x *= r; b.y *= r; b.z *= r; b.w *= r;
+        } else if (t < tokens) {
+          const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
+          a = src[0];
+          b = src[1];
+          if (fz.norm) wn = *reinterpret_cast<const uint4*>(fz.norm + wi * 8);
         }
-        xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
-        bias += dpp<0xB1>(0.f, bias);
-        bias += dpp<0x4E>(0.f, bias);
-        if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
-      } else {
-        xs4[(t * 8 + 2 * j) * nch + c] = a;
-        xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
-        xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        stage(t, wi, a, b, wn);
       }
     }
   }
@@ -496,12 +534,12 @@ inline int gemv_blocks(int64_t n_out, int ro) {
   return b > 1024 ? 1024 : (int)b;
 }
 
-template <bool G32, int R, int T, int MODE, int D>
+template <bool G32, int R, int T, int MODE, int D, int XR>
 static int launch_d(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
                     int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
   constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
   const size_t lds = (size_t)T * k * sizeof(float) + (size_t)T * (k / 8) * sizeof(float);
-  auto kern = k_gemv_q4<G32, R, T, MODE, D>;
+  auto kern = k_gemv_q4<G32, R, T, MODE, D, XR>;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
@@ -510,6 +548,17 @@ static int launch_d(const uint32_t* wq, const uint16_t* ws, const float* x, floa
   const int blocks = gemv_blocks(n_out, RO);
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, wq, ws, x, y, n_out, k, group, f, tokens, moe, fz);
   return launch_status();
+}
+
+// x in registers (XR words per thread) for one token of x (not split-attention states) with K <= 8192.
+template <bool G32, int R, int T, int MODE, int D>
+static int launch_x(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
+                    int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
+  if constexpr (T == 1 && MODE != kMoeDown) {
+    if (!fz.parts && k <= 2048) return launch_d<G32, R, T, MODE, D, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    if (!fz.parts && k <= 8192) return launch_d<G32, R, T, MODE, D, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  }
+  return launch_d<G32, R, T, MODE, D, 0>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
 }
 
 // Pipeline depth of the dense G32 modes: the chunks one wave streams (per lane: K/2048 per row block, times its row
@@ -522,10 +571,10 @@ static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, floa
     constexpr int RO = MODE == kGateUp ? R / 2 : R;
     const int64_t waves = 4 * (int64_t)gemv_blocks(n_out, RO);
     const int64_t items = ((k / 32 + 63) / 64) * ((n_out + waves * RO - 1) / (waves * RO));
-    if (items >= 4 && R <= 2) return launch_d<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
-    if (items >= 2) return launch_d<G32, R, T, MODE, 2>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    if (items >= 4 && R <= 2) return launch_x<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    if (items >= 2) return launch_x<G32, R, T, MODE, 2>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   }
-  return launch_d<G32, R, T, MODE, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  return launch_x<G32, R, T, MODE, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
 }
 
 // Weight rows per wave iteration. Measured on MI355X (G = 32, K = 2048): R = 2 is fastest while the matrix has fewer
