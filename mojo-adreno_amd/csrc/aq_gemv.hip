@@ -65,7 +65,8 @@ __device__ __forceinline__ int gemv_row(int base, int r, int n_out, int f, const
 // D: register sets of the chunk pipeline (dense G32 modes), chosen at launch from the chunks a wave has.
 // XR: one token, K <= 256 * XR * 8, x given (not split-attention states): each thread requests its XR words of x
 // into registers before the weights, so their staging overlaps the weights' arrival (vector memory completes in
-// order: x requested after the weights would wait for them). 0: x is loaded while it is staged.
+// order: x requested after the weights would wait for them). -1: the same for split-attention states (one word of
+// x, i.e. K <= 2048). 0: x is loaded while it is staged.
 template <bool G32, int R, int T, int MODE, int D, int XR>
 __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
@@ -194,6 +195,24 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   constexpr int kXi = XR > 0 ? XR : 1;
   float4 xra[kXi], xrb[kXi];
   uint4 xrn[kXi];
+  float2 pml_r[AQ_ATTN_MAX_SPLITS];  // XR < 0: (m, l) of each split of this word's head, and its 8 partial outputs
+  float4 poa_r[AQ_ATTN_MAX_SPLITS], pob_r[AQ_ATTN_MAX_SPLITS];
+  if constexpr (XR < 0) {
+    const int S = fz.splits;
+    const uint32_t wi = threadIdx.x, h = wi >> 3, d0 = (wi & 7) * 8;
+    const bool ok = wi < (uint32_t)kw;
+    const uint32_t o_bytes = (uint32_t)(k / 64) * S * 64 * 4;
+    const __amdgpu_buffer_rsrc_t p_rsrc = make_rsrc(fz.parts, o_bytes + (uint32_t)(k / 64) * S * 2 * 4);
+#pragma unroll
+    for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
+      const bool use = ok && cc < S;
+      const uint32_t oo = ((h * S + cc) * 64 + d0) * 4;
+      pml_r[cc] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                 p_rsrc, use ? o_bytes + (h * S + cc) * 8 : kOOB, 0, 0));
+      poa_r[cc] = __builtin_bit_cast(float4, buf_load16(p_rsrc, use ? oo : kOOB));
+      pob_r[cc] = __builtin_bit_cast(float4, buf_load16(p_rsrc, use ? oo + 16 : kOOB));
+    }
+  }
   if constexpr (XR > 0) {
     // the norm weights first: a wait for x, which comes after them, then covers them, whether or not they exist
     if (fz.norm) {
@@ -280,7 +299,36 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       xsum[(t * 4 + j) * nch + c] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
     }
   };
-  if constexpr (XR > 0) {
+  // the attention output for 8 dimensions from the splits' states: sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c
+  auto combine = [&](const float2 (&ml)[AQ_ATTN_MAX_SPLITS], const float4 (&oa)[AQ_ATTN_MAX_SPLITS],
+                     const float4 (&ob)[AQ_ATTN_MAX_SPLITS], float4& a, float4& b) {
+    const int S = fz.splits;
+    float mx = ml[0].x;
+#pragma unroll
+    for (int cc = 1; cc < AQ_ATTN_MAX_SPLITS; ++cc) mx = cc < S ? fmaxf(mx, ml[cc].x) : mx;
+    float den = 0.f;
+    a = make_float4(0.f, 0.f, 0.f, 0.f);
+    b = a;
+#pragma unroll
+    for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
+      const float w = cc < S ? expf(ml[cc].x - mx) : 0.f;  // a split with no positions has m = -inf: weight 0
+      den = fmaf(w, ml[cc].y, den);
+      a.x = fmaf(w, oa[cc].x, a.x); a.y = fmaf(w, oa[cc].y, a.y);
+      a.z = fmaf(w, oa[cc].z, a.z); a.w = fmaf(w, oa[cc].w, a.w);
+      b.x = fmaf(w, ob[cc].x, b.x); b.y = fmaf(w, ob[cc].y, b.y);
+      b.z = fmaf(w, ob[cc].z, b.z); b.w = fmaf(w, ob[cc].w, b.w);
+    }
+    const float r = 1.0f / den;
+    a.x *= r; a.y *= r; a.z *= r; a.w *= r;
+    b.x *= r; b.y *= r; b.z *= r; b.w *= r;
+  };
+  if constexpr (XR < 0) {
+    if ((int)threadIdx.x < kw) {
+      float4 a, b;
+      combine(pml_r, poa_r, pob_r, a, b);
+      stage(0, threadIdx.x, a, b, make_uint4(0u, 0u, 0u, 0u));
+    }
+  } else if constexpr (XR > 0) {
 #pragma unroll
     for (int i = 0; i < kXi; ++i) {
       const int wi = threadIdx.x + 256 * i;
@@ -295,33 +343,17 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
         if (fz.parts) {  // workgroup-uniform; one token: dimensions 8 (wi % 8) .. + 7 of head wi / 8
           const int h = wi >> 3, d0 = (wi & 7) * 8, S = fz.splits;
           const float* po = fz.parts + (size_t)h * S * 64 + d0;
-          const float* pml = fz.parts + (size_t)(k / 64) * S * 64 + (size_t)h * S * 2;
-          float mv[AQ_ATTN_MAX_SPLITS], lv[AQ_ATTN_MAX_SPLITS];
+          const float* pm = fz.parts + (size_t)(k / 64) * S * 64 + (size_t)h * S * 2;
+          float2 ml[AQ_ATTN_MAX_SPLITS];
           float4 oa[AQ_ATTN_MAX_SPLITS], ob[AQ_ATTN_MAX_SPLITS];
 #pragma unroll
           for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {  // all requests first
             const int ci = cc < S ? cc : 0;
-            mv[cc] = pml[2 * ci];
-            lv[cc] = pml[2 * ci + 1];
+            ml[cc] = make_float2(pm[2 * ci], pm[2 * ci + 1]);
             oa[cc] = *reinterpret_cast<const float4*>(po + ci * 64);
             ob[cc] = *reinterpret_cast<const float4*>(po + ci * 64 + 4);
           }
-          float mx = mv[0];
-#pragma unroll
-          for (int cc = 1; cc < AQ_ATTN_MAX_SPLITS; ++cc) mx = cc < S ? fmaxf(mx, mv[cc]) : mx;
-          float den = 0.f;
-#pragma unroll
-          for (int cc = 0; cc < AQ_ATTN_MAX_SPLITS; ++cc) {
-            const float w = cc < S ? expf(mv[cc] - mx) : 0.f;  // a split with no positions has m = -inf: weight 0
-            den = fmaf(w, lv[cc], den);
-            a.x = fmaf(w, oa[cc].x, a.x); a.y = fmaf(w, oa[cc].y, a.y);
-            a.z = fmaf(w, oa[cc].z, a.z); a.w = fmaf(w, oa[cc].w, a.w);
-            b.x = fmaf(w, ob[cc].x, b.x); b.y = fmaf(w, ob[cc].y, b.y);
-            b.z = fmaf(w, ob[cc].z, b.z); b.w = fmaf(w, ob[cc].w, b.w);
-          }
-          const float r = 1.0f / den;
-          a.x *= r; a.y *= r; a.z *= r; a.w *= r;
-          b.x *= r; b.y *= r; b.z *= r; b.w *= r;
+          combine(ml, oa, ob, a, b);
         } else if (t < tokens) {
           const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * k + wi * 8);
           a = src[0];
@@ -555,6 +587,9 @@ template <bool G32, int R, int T, int MODE, int D>
 static int launch_x(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
                     int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
   if constexpr (T == 1 && MODE != kMoeDown) {
+    if constexpr (MODE == kAdd && G32) {  // the attention output projection
+      if (fz.parts && k <= 2048) return launch_d<G32, R, T, MODE, D, -1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    }
     if (!fz.parts && k <= 2048) return launch_d<G32, R, T, MODE, D, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
     if (!fz.parts && k <= 8192) return launch_d<G32, R, T, MODE, D, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   }
