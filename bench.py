@@ -1,7 +1,7 @@
 """Benchmark of the weight-quantized matmul path on one MI355X; prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-    python bench.py --profile dominant|copy     # short runs for rocprofv3 --pmc passes
+    python bench.py --profile dominant|copy|decode   # short runs for rocprofv3 passes
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
   value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
@@ -212,6 +212,8 @@ def profile_run(dev, what: str):
         launches = _gate_up_launches(dev)
         for fn in launches:
             fn()
+    elif what == "decode":  # C4: 20 graph-replayed decode steps at context 512
+        bench_decode_c4(dev, replays=20)
     else:
         nbytes = 256 << 20
         a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -392,7 +394,8 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("dominant", "copy"), help="short run for a rocprofv3 counter pass")
+    ap.add_argument("--profile", choices=("dominant", "copy", "decode"),
+                    help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, or C4 decode steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",

@@ -271,7 +271,8 @@ __global__ __launch_bounds__(kAttnT) void k_attn_decode(const float* __restrict_
 // projection, so the 8 KV heads spread over 8 * splits workgroups with no extra launch.
 //   parts  o: [heads][splits][64] floats, then m, l: [heads][splits][2] floats
 // A split past the last position writes m = -inf, l = 0, o = 0. The split holding pos does RoPE of the key and the
-// cache append (and uses that row from LDS); every split rotates the queries itself.
+// cache append (and uses that row from LDS); every split rotates the queries itself. The span's first rows and the
+// q, k, v values are requested before the position is read (they do not depend on it).
 template <int HPG>
 __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qkv, const float* __restrict__ cosb,
                                                     const float* __restrict__ sinb, uint16_t* kc, uint16_t* vc,
@@ -286,8 +287,28 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
   __shared__ float pv[kT / 16][HPG][kHd];
   const int g = blockIdx.x, sp = blockIdx.y, splits = gridDim.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int pos = *pos_p;
   const int s0 = sp * span;
+  const int c = t & 7, pg = t >> 3;
+  const size_t cbase = (size_t)g * max_pos * kHd;
+  const uint16_t* kbase = kc + cbase + 8 * c;
+  const uint16_t* vbase = vc + cbase + 8 * c;
+  // Requests that do not depend on the position go out before it is read: the span's first cached rows (two of each
+  // per thread; rows past the position hold stale values and are masked below, row pos is taken from LDS) and this
+  // head group's q, k, v.
+  uint4 kr[2], vr[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const size_t row = (size_t)min(s0 + pg + kStride * i, max_pos - 1) * kHd;
+    kr[i] = *reinterpret_cast<const uint4*>(kbase + row);
+    vr[i] = *reinterpret_cast<const uint4*>(vbase + row);
+  }
+  const int qi = t % kHalf;
+  const float* qp = qkv + (size_t)(g * HPG + min(t / kHalf, HPG - 1)) * kHd;
+  const float qa = qp[qi], qb = qp[qi + kHalf];
+  const float* kp = qkv + (size_t)heads * kHd + g * kHd;
+  const float* vp = qkv + (size_t)(heads + kv_heads) * kHd + g * kHd;
+  const float ka = kp[qi], kb = kp[qi + kHalf], va = vp[qi], vb = vp[qi + kHalf];
+  const int pos = *pos_p;
   float* po = parts + (size_t)g * HPG * splits * kHd;                       // o of head g*HPG + h, split sp
   float* pml = parts + (size_t)heads * splits * kHd + (size_t)g * HPG * splits * 2;
   if (pos < 0 || pos >= max_pos || s0 > pos) {  // workgroup-uniform: no position here
@@ -300,36 +321,18 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
   }
   const int s1 = min(s0 + span, pos + 1);  // this split's positions: [s0, s1)
   const bool mine = pos < s0 + span;       // holds position pos: rotates and stores its key and value
-  const size_t cbase = (size_t)g * max_pos * kHd;
-  const int c = t & 7, pg = t >> 3;
-  const uint16_t* kbase = kc + cbase + 8 * c;
-  const uint16_t* vbase = vc + cbase + 8 * c;
   const int passes = (s1 - s0 + 2 * kStride - 1) / (2 * kStride);
 
-  // the first pass's rows (two of each per thread), requested before RoPE; rows past pos re-read row pos
-  uint4 kr[2], vr[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const size_t row = (size_t)min(s0 + pg + kStride * i, pos) * kHd;
-    kr[i] = *reinterpret_cast<const uint4*>(kbase + row);
-    vr[i] = *reinterpret_cast<const uint4*>(vbase + row);
-  }
+  const float cs = cosb[pos * kHalf + qi], sn = sinb[pos * kHalf + qi];
   if (t < HPG * kHalf) {
-    const int hh = t / kHalf, i = t % kHalf;
-    const float* q = qkv + (size_t)(g * HPG + hh) * kHd;
-    const float a = q[i], b = q[i + kHalf];
-    const float cs = cosb[pos * kHalf + i], sn = sinb[pos * kHalf + i];
-    qs[hh][i] = a * cs - b * sn;
-    qs[hh][i + kHalf] = b * cs + a * sn;
+    const int hh = t / kHalf;
+    qs[hh][qi] = qa * cs - qb * sn;
+    qs[hh][qi + kHalf] = qb * cs + qa * sn;
   }
   if (mine && t >= kT - kHalf) {  // the last 32 threads (with 8 query heads they also rotated a query pair)
-    const int i = t - (kT - kHalf);
-    const float* kp = qkv + (size_t)heads * kHd + g * kHd;
-    const float* vp = qkv + (size_t)(heads + kv_heads) * kHd + g * kHd;
-    const float a = kp[i], b = kp[i + kHalf];
-    const float cs = cosb[pos * kHalf + i], sn = sinb[pos * kHalf + i];
-    const uint16_t k0 = float_to_half_bits(a * cs - b * sn), k1 = float_to_half_bits(b * cs + a * sn);
-    const uint16_t v0 = float_to_half_bits(vp[i]), v1 = float_to_half_bits(vp[i + kHalf]);
+    const int i = qi;
+    const uint16_t k0 = float_to_half_bits(ka * cs - kb * sn), k1 = float_to_half_bits(kb * cs + ka * sn);
+    const uint16_t v0 = float_to_half_bits(va), v1 = float_to_half_bits(vb);
     uint16_t* kd = kc + cbase + (size_t)pos * kHd;
     uint16_t* vd = vc + cbase + (size_t)pos * kHd;
     kd[i] = k0;
