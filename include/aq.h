@@ -38,12 +38,14 @@ int aq_version(void);
 
 /* ---- int4 (Q4W) matrix-vector products, decode ------------------------------------------------------------------
  * y[t, n] = (add ? y[t, n] : 0) + sum_k W[n, k] * x[t, k] for t < tokens, fp32 x [tokens, K] and y [tokens, N].
- * tokens = 1 is the decode GEMV; tokens <= 8 the few-token form. Every weight word is read once per launch for
- * all tokens.
+ * tokens = 1 is the decode GEMV; tokens <= 16 the few-row form (a weight row read once for all rows). Every weight
+ * word is read once per launch for all tokens.
  * Replaces: gemv_q4 (llama/kernels/gemv_q4.mojo:13-30, G=64), gemv_add_q4 (llama/kernels/gemv_add_q4.mojo:13-30,
  * add=1), lk.gemv_q4[B] (lfm2/kernels/lk.mojo:134-143, G=32), moek.p_gemv_q4 / t_gemv_q4
- * (qwen3moe/kernels/moek.mojo:273-281,528-545: tokens, add).
- * Requires K % 32 == 0, K % group == 0, group % 8 == 0, tokens in 1..8, K*tokens <= 32768, 16-byte aligned wq/x. */
+ * (qwen3moe/kernels/moek.mojo:273-281,528-545: tokens, add), and the few-row products rows_q4 (lfm2/kernels/dsk.mojo:
+ * 97-119, count <= 12, speculative verify).
+ * Requires K % 32 == 0, K % group == 0, group % 8 == 0, tokens in 1..16, K * (tokens rounded up to 1, 2, 4, 8 or 16)
+ * <= 32768, 16-byte aligned wq/x. */
 int aq_gemv_q4(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int64_t n, int64_t k,
                int32_t group, int32_t tokens, int32_t add, void* stream);
 
@@ -152,6 +154,18 @@ int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float*
                void* workspace, int64_t workspace_bytes, void* stream);
 int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);
 
+/* Ternary output head with greedy argmax on the device: logits = the aq_t2_gemv product over the vocabulary rows,
+ * each workgroup also leaving the argmax key of its columns in cand (aq_t2_head_candidates(n) of them, 8-byte
+ * aligned); then *token = the first index of the largest logit, or -1 when any logit is NaN or infinite,
+ * hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance. Replaces: packed_head with
+ * select = 1 (bonsai/kernels/kernels.mojo:451-517: logits plus per-64-lane (best, index, nonfinite) candidates) and
+ * the host's greedy() over them (bonsai/bonsai_vk.c:506-515: largest value, lowest index on ties; a nonfinite flag
+ * stops it with "nonfinite logits"). */
+int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* logits, int64_t n, int64_t k,
+                      uint64_t* cand, int64_t cand_cap, int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap,
+                      int32_t advance, void* stream);
+int64_t aq_t2_head_candidates(int64_t n);
+
 /* partials[g, n] = sum over k in [1024 g, 1024 g + 1024) of the products above, g < ceil(K/1024).
  * Replaces: packed_linear (bonsai/kernels/kernels.mojo:283-325; its grid (ceil(N/64), ceil(K/1024))). */
 int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials, int64_t n,
@@ -225,8 +239,9 @@ int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, i
 
 /* Final norm, lm_head and greedy argmax: logits = W . rmsnorm(x) (norm_w NULL: x as given), then *token = the first
  * index of the largest logit, hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance.
- * cand: device scratch of AQ_HEAD_CANDIDATES argmax keys (8-byte aligned). Replaces: Llama.head
- * (llama/model.mojo:160-166) and the host argmax scan (llama/llama.mojo:72-75). */
+ * cand: device scratch of AQ_HEAD_CANDIDATES argmax keys (8-byte aligned). NaN logits never win, as in the
+ * reference's `logits[i] > logits[best]` scan (which differs only when logit 0 itself is NaN: it then returns 0).
+ * Replaces: Llama.head (llama/model.mojo:160-166) and the host argmax scan (llama/llama.mojo:72-75). */
 #define AQ_HEAD_CANDIDATES 4096
 int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w, float eps,
                       float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand, int64_t cand_cap,

@@ -37,6 +37,8 @@ SIGNATURES: dict[str, list] = {
     "aq_gemv_f32": [_p, _p, _p, _i64, _i64, _i32, _p],
     "aq_t2_gemv": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p],
     "aq_t2_gemv_workspace_bytes": [_i64, _i64],
+    "aq_t2_head_argmax": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
+    "aq_t2_head_candidates": [_i64],
     "aq_t2_packed_linear": [_p, _p, _p, _p, _i64, _i64, _p],
     "aq_t2_packed_reduce": [_p, _p, _i64, _i32, _p],
     "aq_pack_half": [_p, _p, _i64, _p],
@@ -57,6 +59,7 @@ SIGNATURES: dict[str, list] = {
     "aq_t2w_from_mlx": [_p, _p, _p, _p, _i32, _i64, _p, _p],
 }
 RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64, "aq_t2_gemv_workspace_bytes": ctypes.c_int64,
+            "aq_t2_head_candidates": ctypes.c_int64,
             "aq_gemm_t2_workspace_bytes": ctypes.c_int64, "aq_moe_group_max_rows": ctypes.c_int64,
             "aq_moe_group_max_tiles": ctypes.c_int32}
 

@@ -126,7 +126,8 @@ def gemm_q4(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, y: torch.Tensor
 
 
 def gemv_q4(wq: torch.Tensor, ws: torch.Tensor, x: torch.Tensor, y: torch.Tensor, group: int, add: bool = False):
-    """``y[t] (+)= deq(W) . x[t]`` for Q4W ``wq [N, K/8]``, fp16 ``ws [N, K/group]``, fp32 ``x [T, K]``, T <= 8."""
+    """``y[t] (+)= deq(W) . x[t]`` for Q4W ``wq [N, K/8]``, fp16 ``ws [N, K/group]``, fp32 ``x [T, K]``, T <= 16
+    (9..16 rows: K <= 2048)."""
     torch.ops.aq.gemv_q4(wq, ws, x, y, group, add)
 
 
@@ -140,6 +141,8 @@ def gate_up_q4(wq: torch.Tensor, ws: torch.Tensor, x: torch.Tensor, a: torch.Ten
 _LIB.define("t2_gemv(Tensor x2h, Tensor w, Tensor s, Tensor(a!) y, Tensor(b!) workspace) -> ()")
 _LIB.define("t2_packed_linear(Tensor x2h, Tensor w, Tensor s, Tensor(a!) partials) -> ()")
 _LIB.define("t2_packed_reduce(Tensor partials, Tensor(a!) y) -> ()")
+_LIB.define("t2_head_argmax(Tensor x2h, Tensor w, Tensor s, Tensor(a!) logits, Tensor(b!) cand, Tensor(c!) token, "
+            "Tensor(d!) pos, Tensor(e!) hist, int advance) -> ()")
 _LIB.define("pack_half(Tensor x, Tensor(a!) q) -> ()")
 _LIB.define("rmsnorm_pack(Tensor x, Tensor w, Tensor(a!) q, float eps) -> ()")
 _LIB.define("swiglu_pack(Tensor gu, Tensor(a!) q) -> ()")
@@ -163,6 +166,21 @@ def _t2_gemv_impl(x2h, w, s, y, workspace):
     _check(y.dtype == torch.float32 and y.numel() == n, "y must be float32 [N]")
     _lib.call("aq_t2_gemv", _ptr(x2h), _ptr(w), _ptr(s), _ptr(y), n, k, _ptr(workspace),
               workspace.numel() * workspace.element_size(), _stream(y))
+
+
+def t2_head_candidates(n: int) -> int:
+    """Argmax keys the ternary head leaves for an N-row vocabulary (one per workgroup)."""
+    return int(_lib.lib().aq_t2_head_candidates(n))
+
+
+def _t2_head_argmax_impl(x2h, w, s, logits, cand, token, pos, hist, advance):
+    n, k = _t2_shapes(x2h, w, s)
+    _dev(logits, cand, token, pos, hist)
+    _check(logits.dtype == torch.float32 and logits.numel() == n, "logits must be float32 [N]")
+    _check(cand.dtype == torch.int64, "cand must be int64")
+    _check(token.dtype == torch.int32 and pos.dtype == torch.int32 and hist.dtype == torch.int32, "int32 token/pos/hist")
+    _lib.call("aq_t2_head_argmax", _ptr(x2h), _ptr(w), _ptr(s), _ptr(logits), n, k, _ptr(cand), cand.numel(),
+              _ptr(token), _ptr(pos), _ptr(hist) if hist.numel() else None, hist.numel(), advance, _stream(logits))
 
 
 def _t2_packed_linear_impl(x2h, w, s, partials):
@@ -210,6 +228,7 @@ def _swiglu_pack_impl(gu, q):
 
 
 _LIB.impl("t2_gemv", _t2_gemv_impl, "CUDA")
+_LIB.impl("t2_head_argmax", _t2_head_argmax_impl, "CUDA")
 _LIB.impl("t2_packed_linear", _t2_packed_linear_impl, "CUDA")
 _LIB.impl("t2_packed_reduce", _t2_packed_reduce_impl, "CUDA")
 _LIB.impl("pack_half", _pack_half_impl, "CUDA")

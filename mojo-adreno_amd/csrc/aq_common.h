@@ -95,6 +95,22 @@ __device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_
   return half_bits_to_float(h);
 }
 
+// Argmax key: larger for a larger value and, among equal values, for a smaller index, so the maximum key names the
+// first maximum (the reference's `if logits[i] > logits[best]` scan). 0 is below every key of a finite value.
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)idx;
+}
+// The key a producer leaves when any of its values is not finite: above every key of a finite value, so the step's
+// maximum is this key exactly when some logit was NaN or infinite (the token is then -1).
+constexpr uint64_t kNonFiniteKey = ~0ull;
+
+// Greedy-decode step end (aq_gemv.hip): the largest of ncand argmax keys becomes *token (and hist[*pos]), -1 when
+// that is kNonFiniteKey, then *pos += advance. One workgroup.
+int launch_argmax_step(const uint64_t* cand, int ncand, int32_t* token, int32_t* pos, int32_t* hist, int hist_cap,
+                       int advance, hipStream_t s);
+
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 inline int launch_status() {

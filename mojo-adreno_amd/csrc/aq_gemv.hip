@@ -38,13 +38,6 @@ struct Fuse {
   int splits;
 };
 
-// Argmax key: larger for a larger value and, among equal values, for a smaller index, so the maximum key names the
-// first maximum (the reference's `if logits[i] > logits[best]` scan). 0 is below every key of a finite value.
-__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
-  uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)idx;
-}
 
 // Weight row r of the output block starting at `base` (every mode but kMoeDown; -1 = no row, kMoeGateUp only). Rows
 // past the end repeat the last output's; their sums are not written.
@@ -399,8 +392,10 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
         if constexpr (MODE == kAdd) v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
       }
-      if constexpr (MODE == kStore) {  // rows arrive in ascending order, so `>` keeps the first maximum
-        if (o < n_out && (best_row < 0 || acc[r][0] > best)) best = acc[r][0], best_row = o;
+      if constexpr (MODE == kStore) {  // rows arrive in ascending order, so `>` keeps the first maximum; NaN rows
+                                       // never win, as in the reference's `logits[i] > logits[best]` scan
+        if (o < n_out && !__builtin_isnan(acc[r][0]) && (best_row < 0 || acc[r][0] > best))
+          best = acc[r][0], best_row = o;
       }
     }
   };
@@ -556,7 +551,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     finish(base, acc);
   }
   if constexpr (MODE == kStore) {
-    if (fz.cand && lane == 0) fz.cand[blockIdx.x * 4 + wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
+    if (fz.cand && lane == 0)
+      fz.cand[blockIdx.x * 4 + wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
   }
 }
 
@@ -636,6 +632,9 @@ static int launch_g(const uint32_t* wq, const uint16_t* ws, const float* x, floa
   if (tokens <= 1) return launch_r<G32, 1, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   if (tokens <= 2) return launch_r<G32, 2, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   if (tokens <= 4) return launch_r<G32, 4, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  if constexpr (MODE == kStore || MODE == kAdd) {  // few-row products up to 16 rows (speculative verify)
+    if (tokens > 8) return launch_r<G32, 16, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+  }
   return launch_r<G32, 8, MODE>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
 }
 
@@ -645,10 +644,11 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
                       const Fuse& fz = Fuse{nullptr, 0.f, nullptr, nullptr, 0}) {
   if (!wq || !ws || !x || !y) return AQ_ERR_NULL;
   if (fz.norm && !aligned(fz.norm, 16)) return AQ_ERR_ALIGN;
-  if (n_out <= 0 || k <= 0 || tokens < 1 || tokens > 8) return AQ_ERR_SHAPE;
+  const int max_tokens = (MODE == kStore || MODE == kAdd) ? 16 : 8;
+  if (n_out <= 0 || k <= 0 || tokens < 1 || tokens > max_tokens) return AQ_ERR_SHAPE;
   if (k % 32) return AQ_ERR_SHAPE;
   if (group <= 0 || group % 8 || k % group) return AQ_ERR_GROUP;
-  const int tp = tokens <= 1 ? 1 : tokens <= 2 ? 2 : tokens <= 4 ? 4 : 8;
+  const int tp = tokens <= 1 ? 1 : tokens <= 2 ? 2 : tokens <= 4 ? 4 : tokens <= 8 ? 8 : 16;
   if ((int64_t)tp * k > 32768) return AQ_ERR_CAPACITY;
   if (n_out > (int64_t)1 << 30) return AQ_ERR_SHAPE;
   // W, its scales and y are addressed through 32-bit buffer offsets below 2 GiB
@@ -681,12 +681,18 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const uint64_t* __restrict
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 16; ++w) m = red[w] > m ? red[w] : m;  // m is red[0] here
-    const int idx = m ? (int)~(uint32_t)m : 0;
+    const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
     const int p = *pos;
     *token = idx;
     if (hist && p >= 0 && p < hist_cap) hist[p] = idx;
     *pos = p + advance;
   }
+}
+
+int launch_argmax_step(const uint64_t* cand, int ncand, int32_t* token, int32_t* pos, int32_t* hist, int hist_cap,
+                       int advance, hipStream_t s) {
+  hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, cand, ncand, token, pos, hist, hist_cap, advance);
+  return launch_status();
 }
 
 }  // namespace aq
@@ -753,9 +759,7 @@ extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const f
   const int st = aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream,
                                             aq::Fuse{norm_w, eps, cand, nullptr, 0});
   if (st != AQ_OK) return st;
-  hipLaunchKernelGGL(aq::k_argmax_step, dim3(1), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), cand, ncand,
-                     token, pos, hist, hist_cap, advance);
-  return aq::launch_status();
+  return aq::launch_argmax_step(cand, ncand, token, pos, hist, hist_cap, advance, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, int32_t splits, float* y,

@@ -131,9 +131,10 @@ __global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict_
 // contiguous runs of whole 128-groups, so a load instruction reads CB consecutive words of 64/CB rows. Phase partials
 // are summed in phase order through LDS (deterministic). x' (scaled fp16 pairs) is staged in LDS once.
 template <int CB>
+// cand != NULL: the workgroup also leaves the argmax key of its CB outputs (first maximum) in cand[blockIdx.x].
 __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
-                                                      int K) {
+                                                      int K, uint64_t* __restrict__ cand) {
   constexpr int PH = 8 * 64 / CB;  // phases per workgroup
   extern __shared__ uint32_t xs[];   // [K/16][8] scaled x pairs
   __shared__ float red[PH][CB];
@@ -197,6 +198,21 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
 #pragma unroll
     for (int p = 0; p < PH; ++p) v += red[p][threadIdx.x];
     y[blockIdx.x * CB + threadIdx.x] = v;
+    if (cand) red[0][threadIdx.x] = v;  // each thread rereads only its own column: no barrier needed before this
+  }
+  if (cand) {  // workgroup-uniform
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int c0 = blockIdx.x * CB, cols = min(CB, N - c0);
+      float best = red[0][0];
+      int bi = 0;
+      bool bad = !__builtin_isfinite(best);
+      for (int j = 1; j < cols; ++j) {
+        if (red[0][j] > best) best = red[0][j], bi = j;
+        bad |= !__builtin_isfinite(red[0][j]);
+      }
+      cand[blockIdx.x] = bad ? kNonFiniteKey : argmax_key(best, c0 + bi);
+    }
   }
 }
 
@@ -294,6 +310,24 @@ extern "C" int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k) {
   return 0;  // the fused kernel reduces inside each workgroup
 }
 
+namespace aq {
+// 32-column blocks when that still gives >= 256 workgroups, else 16 (more workgroups, 64-byte segments)
+inline int t2_cols_per_block(int64_t n) { return (n + 31) / 32 >= 256 ? 32 : 16; }
+
+static int launch_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int N, int K,
+                          uint64_t* cand, hipStream_t sm) {
+  const size_t lds = (size_t)(K / 16) * 8 * 4;  // x' staging: 8 scaled pairs per 16-k row = 2K bytes
+  if (lds > 64 * 1024) return AQ_ERR_CAPACITY;
+  if (t2_cols_per_block(N) == 32)
+    hipLaunchKernelGGL(k_t2_gemv_cols<32>, dim3((unsigned)((N + 31) / 32)), dim3(512), lds, sm, x2h, w, s, y, N, K,
+                       cand);
+  else
+    hipLaunchKernelGGL(k_t2_gemv_cols<16>, dim3((unsigned)((N + 15) / 16)), dim3(512), lds, sm, x2h, w, s, y, N, K,
+                       cand);
+  return launch_status();
+}
+}  // namespace aq
+
 extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int64_t n, int64_t k,
                           void* workspace, int64_t workspace_bytes, void* stream) {
   (void)workspace;
@@ -301,16 +335,27 @@ extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t
   int st = t2_check(x2h, w, s, n, k);
   if (st) return st;
   if (!y) return AQ_ERR_NULL;
-  const size_t lds = (size_t)(k / 16) * 8 * 4;  // x' staging: 8 scaled pairs per 16-k row = 2K bytes
-  if (lds > 64 * 1024) return AQ_ERR_CAPACITY;
-  const int N = (int)n, K = (int)k;
+  return launch_t2_gemv(x2h, w, s, y, (int)n, (int)k, nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t aq_t2_head_candidates(int64_t n) {
+  return n > 0 ? (n + aq::t2_cols_per_block(n) - 1) / aq::t2_cols_per_block(n) : 0;
+}
+
+extern "C" int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* logits, int64_t n,
+                                 int64_t k, uint64_t* cand, int64_t cand_cap, int32_t* token, int32_t* pos,
+                                 int32_t* hist, int32_t hist_cap, int32_t advance, void* stream) {
+  int st = t2_check(x2h, w, s, n, k);
+  if (st) return st;
+  if (!logits || !cand || !token || !pos) return AQ_ERR_NULL;
+  if (hist_cap < 0) return AQ_ERR_SHAPE;
+  const int64_t ncand = aq_t2_head_candidates(n);
+  if (cand_cap < ncand) return AQ_ERR_CAPACITY;
+  if (!aligned(cand, 8)) return AQ_ERR_ALIGN;
   hipStream_t sm = reinterpret_cast<hipStream_t>(stream);
-  // 32-column blocks when that still gives >= 256 workgroups, else 16 (more workgroups, 64-byte segments)
-  if ((N + 31) / 32 >= 256)
-    hipLaunchKernelGGL(k_t2_gemv_cols<32>, dim3((unsigned)((N + 31) / 32)), dim3(512), lds, sm, x2h, w, s, y, N, K);
-  else
-    hipLaunchKernelGGL(k_t2_gemv_cols<16>, dim3((unsigned)((N + 15) / 16)), dim3(512), lds, sm, x2h, w, s, y, N, K);
-  return launch_status();
+  st = launch_t2_gemv(x2h, w, s, logits, (int)n, (int)k, cand, sm);
+  if (st != AQ_OK) return st;
+  return launch_argmax_step(cand, (int)ncand, token, pos, hist, hist_cap, advance, sm);
 }
 
 extern "C" int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials,

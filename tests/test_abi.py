@@ -56,7 +56,9 @@ def test_gemv_rejects_bad_shapes_before_launch():
     assert lib.aq_gemv_q4(p, p, p, p, 8, 500, 32, 1, 0, None) == 1      # K % 32 != 0
     assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 12, 1, 0, None) == 2      # group % 8 != 0
     assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 48, 1, 0, None) == 2      # K % group != 0
-    assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 32, 9, 0, None) == 1      # tokens > 8
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 512, 32, 17, 0, None) == 1     # tokens > 16
+    assert lib.aq_gemv_q4(p, p, p, p, 8, 4096, 32, 9, 0, None) == 6     # 16 rows of x staging exceed LDS
+    assert lib.aq_gate_up_q4(p, p, p, p, 8, 512, 32, 9, None) == 1      # gate|up: at most 8 tokens
     assert lib.aq_gemv_q4(p, p, p, p, 0, 512, 32, 1, 0, None) == 1      # N == 0
     assert lib.aq_gemv_q4(p, p, p, p, 8, 32768, 32, 2, 0, None) == 6    # x staging exceeds LDS
     assert lib.aq_gemv_q4(p + 4, p, p, p, 8, 512, 32, 1, 0, None) == 3  # misaligned words
@@ -106,3 +108,21 @@ def test_decode_ops_registered():
     from aq import ops  # noqa: F401
     for name in ("rmsnorm_gemv_q4", "rmsnorm_gate_up_q4", "embed_f16", "attn_decode", "head_argmax_q4"):
         assert hasattr(torch.ops.aq, name)
+
+
+def test_t2_head_argmax_validation():
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    # one argmax key per workgroup: 32 columns each once that gives >= 256 workgroups, else 16
+    assert lib.aq_t2_head_candidates(151669) == 4740
+    assert lib.aq_t2_head_candidates(8000) == 500
+    assert lib.aq_t2_head_candidates(8192) == 256
+    assert lib.aq_t2_head_candidates(7) == 1
+    assert lib.aq_t2_head_candidates(0) == 0
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 499, p, p, None, 0, 1, None) == 6   # too few keys
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 500, p, None, None, 0, 1, None) == 5  # no pos
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p + 4, 500, p, p, None, 0, 1, None) == 3  # misaligned keys
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1000, p, 500, p, p, None, 0, 1, None) == 1     # K % 128
+    assert lib.aq_t2_head_argmax(p, p, p, None, 8000, 1024, p, 500, p, p, None, 0, 1, None) == 5  # no logits

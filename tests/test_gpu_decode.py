@@ -156,6 +156,35 @@ def test_head_argmax_ties_pick_the_first(dev):
     assert int(tok.item()) == 3 and int(pos.item()) == 0
 
 
+def test_head_argmax_skips_nan_rows(dev):
+    """A NaN logit (row 777's scales are NaN) never wins, as in the reference's `logits[i] > logits[best]` scan; an
+    infinite one (row 50) does."""
+    import torch
+    rng = np.random.default_rng(2)
+    vocab, k = 5000, 256
+    wq, ws = _int4(rng, vocab, k)
+    ws[777] = np.float16("nan")
+    x = rng.standard_normal(k).astype(np.float32)
+    logits = torch.empty(vocab, dtype=torch.float32, device=dev)
+    cand = torch.zeros(4096, dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    empty = torch.empty(0, dtype=torch.int32, device=dev)
+    nonorm = torch.empty(0, dtype=torch.float16, device=dev)
+    args = (to_dev(x, dev), nonorm, 1e-5, logits, 32, cand, tok, pos, empty, 0)
+    torch.ops.aq.head_argmax_q4(to_dev(wq, dev), to_dev(ws, dev), *args)
+    lg = to_np(logits)
+    assert np.isnan(lg[777]) and np.isfinite(np.delete(lg, 777)).all()
+    assert int(tok.item()) == orc.argmax_first(np.where(np.isnan(lg), -np.inf, lg))
+    ws[50] = np.float16("inf")
+    wq[50] = 0xFFFFFFFF  # every value -1 * inf * x: +-inf, NaN only where x is 0
+    x = np.abs(x) + 0.5
+    x *= -1  # (-1) * inf * (-x) = +inf for every k
+    torch.ops.aq.head_argmax_q4(to_dev(wq, dev), to_dev(ws, dev), to_dev(x, dev), *args[1:])
+    lg = to_np(logits)
+    assert lg[50] == np.inf and int(tok.item()) == 50
+
+
 def _small_cfg(**kw):
     from aq.llama import LlamaConfig
     base = dict(dim=512, layers=2, heads=8, kv_heads=2, head_dim=64, ffn=1024, vocab=1000, max_pos=64)

@@ -30,6 +30,7 @@ def test_c0_shape_parity(dev):
     (64, 2048, 32, 1), (300, 2048, 64, 1), (129, 768, 128, 1), (77, 8192, 32, 1), (5, 32, 32, 1),
     (33, 4096 + 32, 32, 1), (40, 256, 256, 1), (17, 512, 16, 1), (19, 1024, 8, 1), (23, 96, 24, 1),
     (70, 2048, 32, 2), (70, 2048, 64, 3), (65, 1024, 32, 5), (31, 2048, 128, 8), (9, 4096, 32, 8),
+    (40, 2048, 32, 9), (33, 1024, 64, 12), (17, 2048, 32, 16), (21, 512, 16, 13),
 ])
 def test_kat_bit_exact(dev, n, k, group, tokens):
     """Integer-exact inputs: the GPU result must equal the exact product bit for bit, whatever the sum order."""
@@ -95,3 +96,19 @@ def test_error_paths(dev):
         _ops().gemv_q4(wq, ws, x[1:], y, 32)
     with pytest.raises(ValueError):
         _ops().gemv_q4(wq, ws, x[:512], y, 48)  # 512 % 48 != 0
+
+
+@pytest.mark.parametrize("tokens,k", [(10, 2048), (12, 2048), (16, 1024)])
+def test_few_rows_vs_oracle(dev, tokens, k):
+    """Few-row products (rows_q4, lfm2/kernels/dsk.mojo:97-119: up to 12 rows for speculative verify; here up to 16):
+    every weight row read once for all rows, rel 1e-3."""
+    import torch
+    from aq import synth
+    rng = np.random.default_rng(tokens * 100 + k)
+    n = 21504 if k == 2048 else 3000
+    wq, ws = synth.int4_matrix(rng, n, k, 32)
+    x = rng.standard_normal((tokens, k)).astype(np.float32)
+    y0 = rng.standard_normal((tokens, n)).astype(np.float32)
+    y = to_dev(y0, dev)
+    _ops().gemv_q4(to_dev(wq, dev), to_dev(ws, dev), to_dev(x, dev), y, 32, add=True)
+    assert rel_inf(to_np(y), orc.gemm_q4(wq, ws, x, 32, y0=y0)) < TOL_FP32

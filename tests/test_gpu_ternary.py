@@ -162,3 +162,76 @@ def test_gemm_t2_add(dev):
     y0 = rng.standard_normal((m, n)).astype(np.float32)
     got = _gemm_t2(x, w, s, dev, add_to=y0)
     assert rel_inf(got, orc.ternary_gemm(x, w, s) + y0) < 1e-2
+
+
+def _head(dev, codes, s, x, hist_len=16, pos0=5):
+    import torch
+    n = codes.shape[0]
+    logits = torch.empty(n, dtype=torch.float32, device=dev)
+    cand = torch.zeros(_ops().t2_head_candidates(n), dtype=torch.int64, device=dev)
+    tok = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
+    hist = torch.full((hist_len,), -9, dtype=torch.int32, device=dev)
+    torch.ops.aq.t2_head_argmax(to_dev(orc.x2h_pack(x), dev), to_dev(orc.t2w_pack(codes), dev), to_dev(s, dev),
+                                logits, cand, tok, pos, hist, 1)
+    return to_np(logits), int(tok.item()), int(pos.item()), to_np(hist)
+
+
+@pytest.mark.parametrize("n,k", [(151669, 256), (8000, 1024), (8192, 512), (7, 128)])
+def test_t2_head_argmax_kat(dev, n, k):
+    """Integer-exact logits, so the token must be the first maximum of the exact products (the reference's greedy()
+    over packed_head candidates)."""
+    rng = np.random.default_rng(n)
+    codes, s, x = _kat(rng, n, k)
+    lg, tok, pos, hist = _head(dev, codes, s, x)
+    exact = _exact(codes, s, x).astype(np.float32)
+    np.testing.assert_array_equal(lg, exact)
+    assert tok == orc.argmax_first(exact) and pos == 6
+    assert hist[5] == tok and (np.delete(hist, 5) == -9).all()
+
+
+def test_t2_head_argmax_ties_pick_the_first(dev):
+    """Columns 3, 40, 900 and 7000 are all +1 codes, the largest product: the token is 3, across workgroups."""
+    rng = np.random.default_rng(3)
+    n, k = 8000, 256
+    codes = rng.integers(0, 3, size=(n, k))
+    codes[[3, 40, 900, 7000]] = 2
+    s = np.ones((k // 128, n), np.float16)
+    x = np.ones(k, np.float32)
+    lg, tok, pos, _ = _head(dev, codes, s, x)
+    np.testing.assert_array_equal(lg, (codes - 1).sum(1).astype(np.float32))
+    assert tok == 3 and pos == 6
+
+
+@pytest.mark.parametrize("bad", ["inf", "nan"])
+def test_t2_head_argmax_nonfinite_gives_minus_one(dev, bad):
+    """A NaN or infinite logit (here from an infinite or NaN scale of column 4321) yields token -1, where the
+    reference's greedy() stops with "nonfinite logits"; the position still advances."""
+    rng = np.random.default_rng(4)
+    n, k = 8000, 256
+    codes, s, x = _kat(rng, n, k)
+    codes[4321] = 2
+    s[:, 4321] = np.float16(bad)
+    lg, tok, pos, hist = _head(dev, codes, s, x)
+    assert not np.isfinite(lg[4321]) and np.isfinite(np.delete(lg, 4321)).all()
+    assert tok == -1 and pos == 6 and hist[5] == -1
+
+
+def test_t2_head_argmax_float_logits(dev):
+    """Random ternary head with fp16 activations: logits vs the oracle, token = first maximum of the GPU logits."""
+    import torch
+    from aq import synth
+    rng = np.random.default_rng(6)
+    n, k = 20000, 2048
+    w, s = synth.ternary_matrix(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    xh = orc.x2h_pack(x)
+    logits = torch.empty(n, dtype=torch.float32, device=dev)
+    cand = torch.zeros(_ops().t2_head_candidates(n), dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    torch.ops.aq.t2_head_argmax(to_dev(xh, dev), to_dev(w, dev), to_dev(s, dev), logits, cand, tok, pos,
+                                torch.empty(0, dtype=torch.int32, device=dev), 0)
+    lg = to_np(logits)
+    assert rel_inf(lg, orc.ternary_gemv(w, s, xh, n, k)) < TOL
+    assert int(tok.item()) == orc.argmax_first(lg) and int(pos.item()) == 0
