@@ -271,6 +271,16 @@ int aq_gguf_q4_0_to_q4w(const uint8_t* blocks, int64_t rows, int64_t cols, uint3
  * Replaces: q4_dequant + the "h4" recipe line of lfm2/convert.c:73-80. */
 int aq_gguf_q4_0_to_f16(const uint8_t* blocks, int64_t rows, int64_t cols, uint16_t* out);
 
+/* GGUF Q6_K (210-byte super-blocks of 256: ql[128] low nibbles, qh[64] high 2-bit pairs, int8 scales[16] one per 16
+ * weights, fp16 d) -> Q6W: q [rows, cols/256, 208] (each super-block's first 208 bytes, unchanged) and d fp16
+ * [rows, cols/256]. cols % 256 == 0. Replaces: the "q6" recipe line of lfm2/convert.c:148-155. */
+int aq_gguf_q6_k_to_q6w(const uint8_t* blocks, int64_t rows, int64_t cols, uint8_t* q, uint16_t* d);
+
+/* GGUF Q6_K -> fp16 [rows, cols]: (d * sc) * (q - 32) in fp32, rounded to fp16, where element 128 h + 32 j + l of a
+ * super-block has q = (nibble j / 2 of ql[64 h + 32 (j % 2) + l]) | (bits 2 j, 2 j + 1 of qh[32 h + l]) << 4 and
+ * sc = scales[8 h + 2 j + l / 16]. Replaces: q6_dequant + the "h6" recipe line of lfm2/convert.c:82-103,163-175. */
+int aq_gguf_q6_k_to_f16(const uint8_t* blocks, int64_t rows, int64_t cols, uint16_t* out);
+
 /* MLX 2-bit projections -> one fused T2W matrix: part p has codes [rows[p], K/16], scales and biases fp16
  * [rows[p], K/128]; w [K/16, sum rows] (transposed), s [K/128, sum rows]. Returns AQ_ERR_ARG, writing nothing, if any
  * group is not ternary (bias != -scale). K % 128 == 0. Replaces: addPacked (qwen3/convert.cpp:39-74). */

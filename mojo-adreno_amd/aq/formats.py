@@ -7,6 +7,8 @@ converters' bytes:
   quantize_q4_searched  qwen3moe/convert.c:120-159 "q4" (least-squared-error scale over d = 6.5 .. 9)
   gguf_q4_0_to_q4w      lfm2/convert.c:59-71 (GGUF Q4_0 -> Q4W words + fp16 scales, G = 32)
   gguf_q4_0_to_f16      lfm2/convert.c:73-80 "h4" (GGUF Q4_0 -> fp16)
+  gguf_q6_k_to_q6w      lfm2/convert.c:148-155 "q6" (GGUF Q6_K -> 208-byte super-blocks + fp16 d apart)
+  gguf_q6_k_to_f16      lfm2/convert.c:82-103 "h6" (GGUF Q6_K -> fp16)
   t2w_from_mlx          qwen3/convert.cpp:39-74 addPacked (MLX 2-bit projections -> one transposed T2W matrix)
 
 Inputs are numpy arrays; bf16 weights are passed as their uint16 bit patterns (numpy has no bf16 type).
@@ -68,6 +70,32 @@ def gguf_q4_0_to_f16(blocks, rows: int, cols: int) -> np.ndarray:
         raise ValueError("Q4_0 data size does not match rows x cols")
     out = np.empty((rows, cols), np.float16)
     _lib.call("aq_gguf_q4_0_to_f16", _ptr(src), rows, cols, _ptr(out))
+    return out
+
+
+def _q6_k_src(blocks, rows: int, cols: int) -> np.ndarray:
+    src = np.ascontiguousarray(np.frombuffer(bytes(blocks), np.uint8) if not isinstance(blocks, np.ndarray)
+                               else blocks.view(np.uint8).reshape(-1))
+    if cols % 256 or src.size != rows * cols // 256 * 210:
+        raise ValueError("Q6_K data size does not match rows x cols (cols % 256 == 0, 210 bytes per 256 weights)")
+    return src
+
+
+def gguf_q6_k_to_q6w(blocks, rows: int, cols: int):
+    """GGUF Q6_K rows (rows * cols / 256 super-blocks of 210 bytes) -> Q6W: q uint8 [rows, cols/256, 208] and
+    d fp16 [rows, cols/256]."""
+    src = _q6_k_src(blocks, rows, cols)
+    q = np.empty((rows, cols // 256, 208), np.uint8)
+    d = np.empty((rows, cols // 256), np.float16)
+    _lib.call("aq_gguf_q6_k_to_q6w", _ptr(src), rows, cols, _ptr(q), _ptr(d))
+    return q, d
+
+
+def gguf_q6_k_to_f16(blocks, rows: int, cols: int) -> np.ndarray:
+    """GGUF Q6_K rows -> fp16 [rows, cols] ((d * sc) * (q - 32) in fp32, rounded)."""
+    src = _q6_k_src(blocks, rows, cols)
+    out = np.empty((rows, cols), np.float16)
+    _lib.call("aq_gguf_q6_k_to_f16", _ptr(src), rows, cols, _ptr(out))
     return out
 
 

@@ -7,6 +7,9 @@
 //   aq_gguf_q4_0_to_q4w      lfm2/convert.c:59-71 q4_block: GGUF Q4_0 blocks -> Q4W words (nib ^ 8, de-interleaved)
 //                            and the fp16 scales unchanged.
 //   aq_gguf_q4_0_to_f16      lfm2/convert.c:73-80 + "h4": (nib - 8) * d in fp32, rounded to fp16.
+//   aq_gguf_q6_k_to_q6w      lfm2/convert.c "q6" (:148-155): GGUF Q6_K super-blocks (210 bytes: ql[128], qh[64],
+//                            int8 scales[16], fp16 d) -> their first 208 bytes [rows, cols/256, 208] and d apart.
+//   aq_gguf_q6_k_to_f16      lfm2/convert.c:82-103 q6_dequant + "h6": (d * sc) * (q - 32) in fp32, rounded to fp16.
 //   aq_t2w_from_mlx          qwen3/convert.cpp:39-74 addPacked: MLX 2-bit codes [n_i, K/16] and scales/biases
 //                            [n_i, K/128] of several projections -> one transposed T2W matrix [K/16, sum n_i] and its
 //                            scales [K/128, sum n_i]; every group must be ternary (bias == -scale).
@@ -185,6 +188,42 @@ extern "C" int aq_gguf_q4_0_to_f16(const uint8_t* blocks, int64_t rows, int64_t 
       out[b * 32 + j] = float_to_half((float)((qs[j] & 15) - 8) * d);
       out[b * 32 + j + 16] = float_to_half((float)((qs[j] >> 4) - 8) * d);
     }
+  }
+  return AQ_OK;
+}
+
+extern "C" int aq_gguf_q6_k_to_q6w(const uint8_t* blocks, int64_t rows, int64_t cols, uint8_t* q, uint16_t* d) {
+  if (!blocks || !q || !d) return AQ_ERR_NULL;
+  if (rows <= 0 || cols <= 0 || cols % 256) return AQ_ERR_SHAPE;
+  const int64_t nb = rows * cols / 256;
+  for (int64_t b = 0; b < nb; ++b) {
+    std::memcpy(q + b * 208, blocks + b * 210, 208);
+    std::memcpy(d + b, blocks + b * 210 + 208, 2);
+  }
+  return AQ_OK;
+}
+
+extern "C" int aq_gguf_q6_k_to_f16(const uint8_t* blocks, int64_t rows, int64_t cols, uint16_t* out) {
+  if (!blocks || !out) return AQ_ERR_NULL;
+  if (rows <= 0 || cols <= 0 || cols % 256) return AQ_ERR_SHAPE;
+  const int64_t nb = rows * cols / 256;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t* blk = blocks + b * 210;
+    uint16_t dh;
+    std::memcpy(&dh, blk + 208, 2);
+    const float dd = half_to_float(dh);
+    uint16_t* y = out + b * 256;
+    // element 128 h + 32 j + l (j = 0..3, l = 0..31) of the super-block: the low (j = 0, 1) or high (j = 2, 3)
+    // nibble of ql[64 h + 32 (j & 1) + l], bits 2 j, 2 j + 1 of qh[32 h + l] above it; scale sc[8 h + 2 j + l / 16]
+    for (int h = 0; h < 2; ++h)
+      for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+          const uint8_t lo = blk[64 * h + 32 * (j & 1) + l];
+          const uint8_t hi = blk[128 + 32 * h + l];
+          const int qv = (int)(((j < 2 ? lo : lo >> 4) & 15) | (((hi >> (2 * j)) & 3) << 4)) - 32;
+          const int8_t sc = (int8_t)blk[192 + 8 * h + 2 * j + l / 16];
+          y[128 * h + 32 * j + l] = float_to_half(dd * (float)sc * (float)qv);
+        }
   }
   return AQ_OK;
 }

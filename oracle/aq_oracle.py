@@ -512,6 +512,44 @@ def gguf_q4_0_dequant(raw: bytes | np.ndarray, rows: int, cols: int) -> np.ndarr
     return (q.astype(np.float32) * d).reshape(rows, cols)
 
 
+def gguf_q6_k_to_q6w(raw: bytes | np.ndarray, rows: int, cols: int):
+    """GGUF Q6_K super-blocks (210 bytes: ql[128], qh[64], int8 scales[16], fp16 d) -> Q6W: the first 208 bytes of
+    each super-block [rows, cols/256, 208] and d fp16 [rows, cols/256] (lfm2/convert.c:148-155, recipe "q6")."""
+    b = np.frombuffer(bytes(raw), np.uint8).reshape(rows, cols // 256, 210)
+    return b[:, :, :208].copy(), b[:, :, 208:].copy().view(np.float16).reshape(rows, cols // 256)
+
+
+def q6w_values(q: np.ndarray, d: np.ndarray):
+    """Q6W -> (q6 - 32 as int [rows, cols], per-16 scales d * sc as float32 [rows, cols/16]).
+
+    Element 128 h + 32 j + l of a super-block (h < 2, j < 4, l < 32) is the low (j < 2) or high nibble of
+    ql[64 h + 32 (j % 2) + l] with bits 2 j, 2 j + 1 of qh[32 h + l] above it, minus 32; its scale is
+    sc[8 h + 2 j + l // 16] (lfm2/convert.c:82-103 ``q6_dequant``; lfm2/kernels/lk.mojo:88-129 ``q6_chunk``).
+    """
+    rows, nb, _ = q.shape
+    ql = q[:, :, :128].reshape(rows, nb, 2, 2, 32).astype(np.int32)   # [.., h, j % 2, l]
+    qh = q[:, :, 128:192].reshape(rows, nb, 2, 1, 32).astype(np.int32)  # [.., h, -, l]
+    sc = q[:, :, 192:208].view(np.int8).reshape(rows, nb, 2, 4, 2).astype(np.float32)  # [.., h, j, l // 16]
+    lo = np.concatenate([ql & 15, ql >> 4], axis=3)                     # j = 0, 1 low nibbles; 2, 3 high
+    hi = (qh >> (2 * np.arange(4).reshape(1, 1, 1, 4, 1))) & 3
+    vals = (lo | (hi << 4)) - 32                                         # [rows, nb, h, j, l]
+    ds = d.astype(np.float32).reshape(rows, nb, 1, 1, 1) * sc            # fp32 d * sc
+    return vals.reshape(rows, nb * 256), ds.reshape(rows, nb * 16)
+
+
+def q6w_dequant(q: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """ggml's Q6_K dequantisation ``(d * sc) * (q - 32)``, float32 step by step (lfm2/convert.c:82-103, as
+    lfm2/kernels/lk.mojo ``embed_q6`` writes it)."""
+    vals, ds = q6w_values(q, d)
+    return (np.repeat(ds, 16, axis=1) * vals.astype(np.float32)).astype(np.float32)
+
+
+def gemv_q6(q: np.ndarray, d: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """``y[r] = E[r] . x`` over a Q6W matrix, float64 of the dequantised weights (lfm2/kernels/lk.mojo:179-191
+    ``head_q6``)."""
+    return q6w_dequant(q, d).astype(np.float64) @ np.asarray(x, np.float64)
+
+
 def mlx_to_t2w(parts, k: int):
     """MLX 2-bit affine matrices -> one fused T2W matrix (qwen3/convert.cpp:39-74, ``addPacked``).
 

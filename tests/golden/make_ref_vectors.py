@@ -1,7 +1,7 @@
 """Golden vectors from the reference's own C weight converters, built from their sources by oracle/Makefile.
 
     make -C oracle                      # builds oracle/_ref/{llama_st2bin, qwen3moe_convert, lfm2_convert}
-    python tests/golden/make_ref_vectors.py
+    python tests/golden/make_ref_vectors.py         # every fixture; `... make_ref_vectors.py q6` the Q6_K one only
 
 Each converter reads raw input bytes at the offsets its recipe names (no real checkpoint is needed), so this script
 writes seeded synthetic inputs, runs the converter on a recipe, reads the output bytes back and stores inputs and
@@ -10,6 +10,7 @@ outputs as small .npz fixtures beside this file:
   ref_st2bin_q4.npz    llama/st2bin.c "q4" (quantize4: s = fp16(max|w| / 7), G = 64) on bf16 rows
   ref_qwen3moe_q4.npz  qwen3moe/convert.c "q4" (least-squared-error scale over d = 6.5 .. 9) for G = 32, 64, 128
   ref_lfm2_q4.npz      lfm2/convert.c "q4" (GGUF Q4_0 -> Q4W words + scales) and "h4" (Q4_0 -> fp16)
+  ref_lfm2_q6.npz      lfm2/convert.c "q6" (GGUF Q6_K -> 208-byte super-blocks + d) and "h6" (Q6_K -> fp16)
 
 The inputs include the cases the quantizers branch on: an all-zero group (scale 0), exact .5 quotients (rintf ties
 to even), fp16-subnormal magnitudes and groups whose max is negative. tests/test_oracle_golden.py checks the oracle
@@ -118,7 +119,45 @@ def lfm2_q4(raw: np.ndarray, rows: int, cols: int):
     return words.copy(), scales.copy(), h.copy()
 
 
-def main():
+def q6_k_blocks(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """Random GGUF Q6_K rows: per 256 weights ql[128], qh[64] random bytes, int8 scales[16] over the whole range
+    (incl. -128, 0, 127) and an fp16 d (incl. 0, negative, subnormal)."""
+    nb = rows * cols // 256
+    b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    sc = b[:, 192:208].view(np.int8)
+    sc[0, :3] = (-128, 0, 127)
+    d = (np.abs(rng.standard_normal(nb)) * 0.002).astype(np.float16)
+    d[0] = 0.0
+    d[1] = -d[1]
+    d[2] = np.float16(3e-7)
+    b[:, 208:] = d.view(np.uint8).reshape(nb, 2)
+    return b.reshape(rows, cols // 256 * 210)
+
+
+def lfm2_q6(raw: np.ndarray, rows: int, cols: int):
+    """lfm2/convert.c recipe lines `q6 <src> <rows> <cols> <out q> <out d>` and `h6 <src> <rows> <cols> <out>`."""
+    with tempfile.TemporaryDirectory() as d:
+        d = Path(d)
+        (d / "model.gguf").write_bytes(raw.tobytes())
+        nb = rows * cols // 256
+        qbytes, dbytes, hbytes = nb * 208, nb * 2, rows * cols * 2
+        (d / "recipe.txt").write_text(f"size {qbytes + dbytes + hbytes}\nq6 0 {rows} {cols} 0 {qbytes}\n"
+                                      f"h6 0 {rows} {cols} {qbytes + dbytes}\n")
+        run("lfm2_convert", [str(d / "model.gguf"), str(d / "recipe.txt"), str(d / "out.bin")])
+        out = (d / "out.bin").read_bytes()
+    q = np.frombuffer(out[:qbytes], np.uint8).reshape(rows, cols // 256, 208)
+    dd = np.frombuffer(out[qbytes:qbytes + dbytes], np.float16).reshape(rows, cols // 256)
+    h = np.frombuffer(out[qbytes + dbytes:qbytes + dbytes + hbytes], np.float16).reshape(rows, cols)
+    return q.copy(), dd.copy(), h.copy()
+
+
+def main(only: str | None = None):
+    if only == "q6":  # the Q6_K fixture alone, from its own seed: the other fixtures stay byte for byte
+        raw = q6_k_blocks(np.random.default_rng(2025), 6, 512)
+        q, d, h = lfm2_q6(raw, 6, 512)
+        np.savez_compressed(HERE / "ref_lfm2_q6.npz", raw=raw, q=q, d=d, h6=h)
+        return 0
+
     rng = np.random.default_rng(2024)
     src = bf16_matrix(rng, 24, 512, 64)
     w, s = st2bin_q4(src)
@@ -134,9 +173,10 @@ def main():
     raw = q4_0_blocks(rng, 12, 256)
     w, s, h = lfm2_q4(raw, 12, 256)
     np.savez_compressed(HERE / "ref_lfm2_q4.npz", raw=raw, words=w, scales=s, h4=h)
+    main("q6")
     for f in sorted(HERE.glob("ref_*.npz")):
         print(f.name, f.stat().st_size, "bytes")
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    sys.exit(main(sys.argv[1] if len(sys.argv) > 1 else None))

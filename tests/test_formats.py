@@ -77,6 +77,32 @@ def test_quantize_q4_searched_vs_oracle(fmt, group):
     np.testing.assert_array_equal(q, q_ref)
 
 
+def test_gguf_q6_k_vs_lfm2(fmt):
+    d = np.load(GOLDEN / "ref_lfm2_q6.npz")
+    raw = d["raw"]
+    rows, cols = raw.shape[0], raw.shape[1] // 210 * 256
+    q, dd = fmt.gguf_q6_k_to_q6w(raw, rows, cols)
+    np.testing.assert_array_equal(q, d["q"])
+    np.testing.assert_array_equal(_u16(dd), _u16(d["d"]))
+    np.testing.assert_array_equal(_u16(fmt.gguf_q6_k_to_f16(raw, rows, cols)), _u16(d["h6"]))
+
+
+def test_gguf_q6_k_vs_oracle_random(fmt):
+    rng = np.random.default_rng(9)
+    rows, cols = 5, 1024
+    raw = rng.integers(0, 256, size=rows * cols // 256 * 210, dtype=np.uint8)
+    d = (rng.standard_normal(rows * cols // 256) * 0.01).astype(np.float16)
+    raw.reshape(-1, 210)[:, 208:] = d.view(np.uint8).reshape(-1, 2)
+    q_ref, d_ref = orc.gguf_q6_k_to_q6w(raw, rows, cols)
+    q, dd = fmt.gguf_q6_k_to_q6w(raw, rows, cols)
+    np.testing.assert_array_equal(q, q_ref)
+    np.testing.assert_array_equal(_u16(dd), _u16(d_ref))
+    h = fmt.gguf_q6_k_to_f16(raw, rows, cols)
+    np.testing.assert_array_equal(_u16(h), _u16(orc.q6w_dequant(q_ref, d_ref).astype(np.float16)))
+    with pytest.raises(ValueError):
+        fmt.gguf_q6_k_to_q6w(raw, rows, 1000)
+
+
 def test_gguf_vs_oracle_random(fmt):
     rng = np.random.default_rng(7)
     rows, cols = 10, 320

@@ -44,6 +44,14 @@ def _check_lfm2(raw, rows, cols, words, scales, h4):
     np.testing.assert_array_equal(h.view(np.uint16), h4.view(np.uint16))
 
 
+def _check_lfm2_q6(raw, rows, cols, q6, d6, h6):
+    q, d = orc.gguf_q6_k_to_q6w(raw, rows, cols)
+    np.testing.assert_array_equal(q, q6)
+    np.testing.assert_array_equal(d.view(np.uint16), d6.view(np.uint16))
+    h = orc.q6w_dequant(q, d).astype(np.float16)
+    np.testing.assert_array_equal(h.view(np.uint16), h6.view(np.uint16))
+
+
 def test_quantize4_vs_st2bin_fixture():
     d = np.load(GOLDEN / "ref_st2bin_q4.npz")
     _check_st2bin(d["src_bf16"], d["words"], d["scales"])
@@ -61,6 +69,36 @@ def test_gguf_q4_0_vs_lfm2_fixture():
     raw = d["raw"]
     rows, cols = raw.shape[0], raw.shape[1] // 18 * 32
     _check_lfm2(raw, rows, cols, d["words"], d["scales"], d["h4"])
+
+
+def test_gguf_q6_k_vs_lfm2_fixture():
+    d = np.load(GOLDEN / "ref_lfm2_q6.npz")
+    raw = d["raw"]
+    rows, cols = raw.shape[0], raw.shape[1] // 210 * 256
+    _check_lfm2_q6(raw, rows, cols, d["q"], d["d"], d["h6"])
+    sc = d["q"][0, 0, 192:208].view(np.int8)
+    assert tuple(sc[:3]) == (-128, 0, 127) and float(d["d"][0, 0]) == 0.0  # the planted extremes
+
+
+def test_q6_values_vs_pointer_walk():
+    """The vectorised Q6_K unpacking against a scalar walk in the reference's own loop shape (two 128-weight halves,
+    four quarter outputs per l, then ql += 64, qh += 32, sc += 8): every element's position, bits and scale."""
+    rng = np.random.default_rng(3)
+    blk = rng.integers(0, 256, 208, dtype=np.uint8)
+    d = np.array([[1.0]], np.float16)
+    vals, ds = orc.q6w_values(blk.reshape(1, 1, 208), d)
+    want_v, want_s = np.zeros(256, int), np.zeros(256)
+    ql, qh, sc = 0, 128, 192
+    for n in (0, 128):
+        for l in range(32):
+            for j, (b, shift, hs) in enumerate([(ql + l, 0, 0), (ql + l + 32, 0, 2), (ql + l, 4, 4),
+                                                (ql + l + 32, 4, 6)]):
+                want_v[n + l + 32 * j] = (((int(blk[b]) >> shift) & 15) | (((int(blk[qh + l]) >> hs) & 3) << 4)) - 32
+                want_s[n + l + 32 * j] = np.int8(blk[sc + l // 16 + 2 * j])
+        ql, qh, sc = ql + 64, qh + 32, sc + 8
+    np.testing.assert_array_equal(vals[0], want_v)
+    np.testing.assert_array_equal(np.repeat(ds[0], 16), want_s)
+    assert vals.min() >= -32 and vals.max() <= 31
 
 
 def test_fixture_plants_rounding_ties():
@@ -86,3 +124,5 @@ def test_live_reference_binaries(seed):
         _check_qwen3moe(src, group, *g.qwen3moe_q4(src, group))
     raw = g.q4_0_blocks(rng, 6, 128)
     _check_lfm2(raw, 6, 128, *g.lfm2_q4(raw, 6, 128))
+    raw = g.q6_k_blocks(rng, 3, 768)
+    _check_lfm2_q6(raw, 3, 768, *g.lfm2_q6(raw, 3, 768))
