@@ -247,6 +247,29 @@ int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, co
                       float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand, int64_t cand_cap,
                       int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap, int32_t advance, void* stream);
 
+/* ---- Q6_K tied head / embedding (Q6W: q [rows, cols/256, 208] bytes, 16-byte aligned, d fp16 [rows, cols/256], as
+ * aq_gguf_q6_k_to_q6w writes them; cols % 256 == 0, rows * cols / 256 * 208 < 2^31) ---- */
+
+/* y[r] = E[r] . x, E the dequantized Q6W matrix ((d * sc) * (q - 32)), x fp32 [cols] (16-byte aligned), y fp32 [rows].
+ * Replaces: head_q6 (lfm2/kernels/lk.mojo:179-191, q6_chunk :88-129). */
+int aq_gemv_q6(const uint8_t* q, const uint16_t* d, const float* x, float* y, int64_t rows, int64_t cols,
+               void* stream);
+
+/* Final norm, Q6_K head and greedy argmax: logits = E . rmsnorm(x) (norm_w NULL: x as given), then as
+ * aq_head_argmax_q4: *token = the first index of the largest logit (NaN never wins), hist[*pos] = *token when
+ * 0 <= *pos < hist_cap, *pos += advance. cand: aq_head_q6_candidates(rows, cols) <= AQ_HEAD_CANDIDATES argmax keys,
+ * 8-byte aligned. Replaces: head_q6 + argmax (lfm2/kernels/lk.mojo:179-221: lowest index among equal maxima). */
+int aq_head_argmax_q6(const uint8_t* q, const uint16_t* d, const float* x, const uint16_t* norm_w, float eps,
+                      float* logits, int64_t rows, int64_t cols, uint64_t* cand, int64_t cand_cap, int32_t* token,
+                      int32_t* pos, int32_t* hist, int32_t hist_cap, int32_t advance, void* stream);
+int64_t aq_head_q6_candidates(int64_t rows, int64_t cols);
+
+/* x[t] = the dequantized row ids[t] of the Q6W matrix, fp32 [ntok, cols] (16-byte aligned), bit-exact
+ * (d * sc) * (q - 32); ids outside [0, rows) read row 0. ids: device int32 [ntok], ntok <= 65535.
+ * Replaces: embed_q6 (lfm2/kernels/lk.mojo:224-232). */
+int aq_embed_q6(const uint8_t* q, const uint16_t* d, int64_t rows, int64_t cols, const int32_t* ids, int32_t ntok,
+                float* x, void* stream);
+
 /* ---- weight-format converters (host code: host pointers, synchronous, no GPU) ----------------------------------
  * They write the layouts above from the reference's source formats, byte for byte as the reference's converters do. */
 

@@ -39,6 +39,10 @@ SIGNATURES: dict[str, list] = {
     "aq_t2_gemv_workspace_bytes": [_i64, _i64],
     "aq_t2_head_argmax": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
     "aq_t2_head_candidates": [_i64],
+    "aq_gemv_q6": [_p, _p, _p, _p, _i64, _i64, _p],
+    "aq_head_argmax_q6": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
+    "aq_head_q6_candidates": [_i64, _i64],
+    "aq_embed_q6": [_p, _p, _i64, _i64, _p, _i32, _p, _p],
     "aq_t2_packed_linear": [_p, _p, _p, _p, _i64, _i64, _p],
     "aq_t2_packed_reduce": [_p, _p, _i64, _i32, _p],
     "aq_pack_half": [_p, _p, _i64, _p],
@@ -61,7 +65,7 @@ SIGNATURES: dict[str, list] = {
     "aq_t2w_from_mlx": [_p, _p, _p, _p, _i32, _i64, _p, _p],
 }
 RESTYPES = {"aq_gemm_q4_workspace_bytes": ctypes.c_int64, "aq_t2_gemv_workspace_bytes": ctypes.c_int64,
-            "aq_t2_head_candidates": ctypes.c_int64,
+            "aq_t2_head_candidates": ctypes.c_int64, "aq_head_q6_candidates": ctypes.c_int64,
             "aq_gemm_t2_workspace_bytes": ctypes.c_int64, "aq_moe_group_max_rows": ctypes.c_int64,
             "aq_moe_group_max_tiles": ctypes.c_int32}
 

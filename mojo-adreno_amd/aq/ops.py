@@ -542,6 +542,70 @@ def _head_argmax_q4_impl(wq, ws, x, norm_w, eps, logits, group, cand, token, pos
               cand.numel(), _ptr(token), _ptr(pos), hp, hist.numel(), advance, _stream(x))
 
 
+# ---- Q6_K tied head / embedding (Q6W: q uint8 [rows, cols/256, 208], d fp16 [rows, cols/256]) -------------------
+
+_LIB.define("gemv_q6(Tensor q, Tensor d, Tensor x, Tensor(a!) y) -> ()")
+_LIB.define("head_argmax_q6(Tensor q, Tensor d, Tensor x, Tensor norm_w, float eps, Tensor(a!) logits, "
+            "Tensor(b!) cand, Tensor(c!) token, Tensor(d!) pos, Tensor(e!) hist, int advance) -> ()")
+_LIB.define("embed_q6(Tensor q, Tensor d, Tensor ids, Tensor(a!) x) -> ()")
+
+
+def head_q6_candidates(rows: int, cols: int) -> int:
+    """Argmax keys the Q6_K head leaves (one per wave, at most HEAD_CANDIDATES)."""
+    return int(_lib.lib().aq_head_q6_candidates(rows, cols))
+
+
+def _q6_shape(q, d):
+    _check(q.dtype == torch.uint8 and q.dim() == 3 and q.shape[2] == 208 and q.is_contiguous(),
+           "q must be contiguous uint8 [rows, cols/256, 208]")
+    _f16bits(d, "d")
+    rows, nb = q.shape[0], q.shape[1]
+    _check(d.numel() == rows * nb, "d must be [rows, cols/256]")
+    return rows, nb * 256
+
+
+def _gemv_q6_impl(q, d, x, y):
+    _dev(q, d, x, y)
+    rows, cols = _q6_shape(q, d)
+    _check(x.dtype == torch.float32 and x.numel() == cols, "x must be float32 [cols]")
+    _check(y.dtype == torch.float32 and y.numel() == rows, "y must be float32 [rows]")
+    _lib.call("aq_gemv_q6", _ptr(q), _ptr(d), _ptr(x), _ptr(y), rows, cols, _stream(x))
+
+
+def _head_argmax_q6_impl(q, d, x, norm_w, eps, logits, cand, token, pos, hist, advance):
+    _dev(q, d, x, logits, cand, token, pos)
+    rows, cols = _q6_shape(q, d)
+    _check(x.dtype == torch.float32 and x.numel() == cols, "x must be float32 [cols]")
+    _check(logits.dtype == torch.float32 and logits.numel() == rows, "logits must be float32 [rows]")
+    _check(cand.dtype == torch.int64, "cand must be int64")
+    _check(token.dtype == torch.int32 and pos.dtype == torch.int32, "token and pos must be int32")
+    nw = 0
+    if norm_w.numel():
+        _dev(norm_w)
+        _f16bits(norm_w, "norm_w")
+        _check(norm_w.numel() == cols, "norm_w must be [cols]")
+        nw = _ptr(norm_w)
+    hp = 0
+    if hist.numel():
+        _dev(hist)
+        _check(hist.dtype == torch.int32, "hist must be int32")
+        hp = _ptr(hist)
+    _lib.call("aq_head_argmax_q6", _ptr(q), _ptr(d), _ptr(x), nw, eps, _ptr(logits), rows, cols, _ptr(cand),
+              cand.numel(), _ptr(token), _ptr(pos), hp, hist.numel(), advance, _stream(x))
+
+
+def _embed_q6_impl(q, d, ids, x):
+    _dev(q, d, ids, x)
+    rows, cols = _q6_shape(q, d)
+    _check(ids.dtype == torch.int32 and ids.numel() >= 1, "ids must be int32 on the device")
+    _check(x.dtype == torch.float32 and x.numel() == ids.numel() * cols, "x must be float32 [len(ids), cols]")
+    _lib.call("aq_embed_q6", _ptr(q), _ptr(d), rows, cols, _ptr(ids), ids.numel(), _ptr(x), _stream(x))
+
+
+for _name, _fn in (("gemv_q6", _gemv_q6_impl), ("head_argmax_q6", _head_argmax_q6_impl), ("embed_q6", _embed_q6_impl)):
+    _LIB.impl(_name, _fn, "CUDA")
+
+
 for _name, _fn in (("rmsnorm_gemv_q4", _rmsnorm_gemv_q4_impl), ("rmsnorm_gate_up_q4", _rmsnorm_gate_up_q4_impl),
                    ("embed_f16", _embed_f16_impl), ("attn_decode", _attn_decode_impl),
                    ("attn_decode_split", _attn_decode_split_impl), ("attn_out_q4", _attn_out_q4_impl),

@@ -25,6 +25,19 @@ QWEN3_MOE = dict(experts=128, hidden=2048, ffn=768, topk=8, group=32)
 C3_TOKENS = 404
 
 
+LFM2_HEAD = dict(vocab=65536, hidden=2048)  # LFM2.5's tied Q6_K embedding / output head
+
+
+def q6_matrix(rng: np.random.Generator, rows: int, cols: int):
+    """Q6W: q uint8 [rows, cols/256, 208] with uniform ql/qh bytes and int8 scales uniform in [-32, 31], and
+    d fp16 [rows, cols/256] = |N(0, 0.001)| + 1e-5 (ggml's Q6_K quantizer gives per-16 scales of that kind)."""
+    nb = cols // 256
+    q = rng.integers(0, 256, size=(rows, nb, 208), dtype=np.uint8)
+    q[:, :, 192:] = rng.integers(-32, 32, size=(rows, nb, 16), dtype=np.int8).view(np.uint8)
+    d = (np.abs(rng.standard_normal((rows, nb), dtype=np.float32) * np.float32(0.001)) + np.float32(1e-5))
+    return q, d.astype(np.float16)
+
+
 def int4_matrix(rng: np.random.Generator, n: int, k: int, group: int = 32):
     """Q4W words [n, k/8] (uniform nibbles) and fp16 scales [n, k/group] = |N(0, 0.02)| + 1e-3."""
     wq = rng.integers(0, 2 ** 32, size=(n, k // 8), dtype=np.uint32)
