@@ -1,7 +1,7 @@
 """Benchmark of the weight-quantized matmul path on one MI355X; prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-    python bench.py --profile dominant|copy|decode   # short runs for rocprofv3 passes
+    python bench.py --profile dominant|copy|decode|heads   # short runs for rocprofv3 passes
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
   value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
@@ -15,6 +15,8 @@ Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEM
             weight copies: graph burst (time per launch) and single cold launch.
   decode_c4 C4 Llama-3.2-1B decode step at context 512 (int4 linears incl. lm_head, fp16 KV cache): tokens/s of
             graph-replayed steps, and GB/s over the 711.9 MB a step must read.
+  heads     output heads with their device argmax (LFM2.5 Q6_K 128000 x 2048, Bonsai ternary 248320 x 2048,
+            Llama int4 128256 x 2048): microseconds and GB/s over weight copies rotating past the Infinity Cache.
 The K timed steps are replayed from hipGraphs.
 Inputs are synthetic (seeded), resident in HBM before the timed region. ``--gpus N`` with N > 1 exits: this build
 measures one GPU.
@@ -214,6 +216,8 @@ def profile_run(dev, what: str):
             fn()
     elif what == "decode":  # C4: 20 graph-replayed decode steps at context 512
         bench_decode_c4(dev, replays=20)
+    elif what == "heads":  # the three output heads with their argmax
+        bench_heads(dev)
     else:
         nbytes = 256 << 20
         a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -341,6 +345,59 @@ def bench_decode_c4(dev, replays: int = 40):
     return out
 
 
+def _q6_bytes(rows, cols):
+    return rows * (cols // 256) * 210 + cols * 4 + rows * 4
+
+
+def bench_heads(dev, pool_mb: int = 640):
+    """Output heads with their device argmax (head GEMV + argmax step, two launches): LFM2.5's Q6_K tied head
+    (128000 x 2048), Bonsai's ternary head (248320 x 2048, X2H input) and Llama-3.2-1B's int4 lm_head (128256 x 2048,
+    G = 32), each over a rotating pool of distinct weight copies larger than the 256 MB Infinity Cache. Bytes a
+    launch: the weights (and their scales), x and the logits."""
+    import torch
+    from aq import ops, synth
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(105)
+    cand = torch.zeros(max(ops.HEAD_CANDIDATES, ops.t2_head_candidates(synth.BONSAI_HEAD["vocab"], synth.BONSAI_HEAD["hidden"])),
+                       dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.empty(0, dtype=torch.int32, device=dev)
+    nonorm = torch.empty(0, dtype=torch.float16, device=dev)
+    out = {}
+
+    def run(name, per, make, launch):
+        copies = max(2, int(pool_mb * 1e6 // per))
+        mats = [make() for _ in range(copies)]
+        t = GraphTimer([lambda m=m: launch(m) for m in mats]).time(replays=5) / copies
+        out[name] = dict(us=round(t * 1e6, 2), gbs=round(per / t / 1e9, 1), frac_hbm=round(per / t / 1e9 / HBM_PEAK_GBS, 4),
+                         mb=round(per / 1e6, 1), pool_copies=copies)
+        del mats
+        torch.cuda.empty_cache()
+
+    v, k = synth.LFM2_HEAD["vocab"], synth.LFM2_HEAD["hidden"]
+    x = torch.randn(k, device=dev, generator=gen)
+    lg = torch.empty(v, dtype=torch.float32, device=dev)
+    run("q6_lfm2", _q6_bytes(v, k),
+        lambda: (torch.randint(0, 256, (v, k // 256, 208), dtype=torch.uint8, device=dev, generator=gen),
+                 (torch.rand((v, k // 256), device=dev, generator=gen) * 1e-3).half()),
+        lambda m: torch.ops.aq.head_argmax_q6(m[0], m[1], x, nonorm, 1e-5, lg, cand, tok, pos, hist, 0))
+    v, k = synth.BONSAI_HEAD["vocab"], synth.BONSAI_HEAD["hidden"]
+    xh = torch.randint(0, 2 ** 14, (k // 2,), dtype=torch.int32, device=dev, generator=gen)
+    lg = torch.empty(v, dtype=torch.float32, device=dev)
+    run("t2_bonsai", _t2_gemv_bytes(v, k),
+        lambda: (torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 16, v), dtype=torch.int32, device=dev, generator=gen),
+                 (torch.rand((k // 128, v), device=dev, generator=gen) * 0.02).half()),
+        lambda m: torch.ops.aq.t2_head_argmax(xh, m[0], m[1], lg, cand, tok, pos, hist, 0))
+    v, k = synth.LLAMA_1B["vocab"], synth.LLAMA_1B["hidden"]
+    lg = torch.empty(v, dtype=torch.float32, device=dev)
+    run("q4_llama", _gemv_bytes(v, k, 32),
+        lambda: (torch.randint(-2 ** 31, 2 ** 31 - 1, (v, k // 8), dtype=torch.int32, device=dev, generator=gen),
+                 (torch.rand((v, k // 32), device=dev, generator=gen) * 0.03 + 1e-3).half()),
+        lambda m: torch.ops.aq.head_argmax_q4(m[0], m[1], x, nonorm, 1e-5, lg, 32, cand, tok, pos, hist, 0))
+    return out
+
+
 def cpu_baseline_decode():
     import numpy as np
     from aq import synth
@@ -394,8 +451,9 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("dominant", "copy", "decode"),
-                    help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, or C4 decode steps")
+    ap.add_argument("--profile", choices=("dominant", "copy", "decode", "heads"),
+                    help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, C4 decode steps or "
+                         "the output heads")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
@@ -417,6 +475,7 @@ def main():
     c2 = bench_ternary_c2(dev)
     c3 = bench_moe_c3(dev)
     c4 = bench_decode_c4(dev)
+    heads = bench_heads(dev)
     dom = time_dominant(dev)
     value = c1["flop"] / c1["t_step"] / 1e12
     achieved = dom["flop"] / dom["t"] / 1e12
@@ -441,6 +500,7 @@ def main():
         "ternary_c2": c2,
         "moe_c3": c3,
         "decode_c4": c4,
+        "heads": heads,
         "wall_s": round(wall, 2),
     }
     if not args.skip_cpu:

@@ -155,7 +155,7 @@ int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float*
 int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);
 
 /* Ternary output head with greedy argmax on the device: logits = the aq_t2_gemv product over the vocabulary rows,
- * each workgroup also leaving the argmax key of its columns in cand (aq_t2_head_candidates(n) of them, 8-byte
+ * each workgroup also leaving the argmax key of its columns in cand (aq_t2_head_candidates(n, k) of them, 8-byte
  * aligned); then *token = the first index of the largest logit, or -1 when any logit is NaN or infinite,
  * hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance. Replaces: packed_head with
  * select = 1 (bonsai/kernels/kernels.mojo:451-517: logits plus per-64-lane (best, index, nonfinite) candidates) and
@@ -164,7 +164,7 @@ int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);
 int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* logits, int64_t n, int64_t k,
                       uint64_t* cand, int64_t cand_cap, int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap,
                       int32_t advance, void* stream);
-int64_t aq_t2_head_candidates(int64_t n);
+int64_t aq_t2_head_candidates(int64_t n, int64_t k);
 
 /* partials[g, n] = sum over k in [1024 g, 1024 g + 1024) of the products above, g < ceil(K/1024).
  * Replaces: packed_linear (bonsai/kernels/kernels.mojo:283-325; its grid (ceil(N/64), ceil(K/1024))). */

@@ -38,7 +38,7 @@ SIGNATURES: dict[str, list] = {
     "aq_t2_gemv": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p],
     "aq_t2_gemv_workspace_bytes": [_i64, _i64],
     "aq_t2_head_argmax": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
-    "aq_t2_head_candidates": [_i64],
+    "aq_t2_head_candidates": [_i64, _i64],
     "aq_gemv_q6": [_p, _p, _p, _p, _i64, _i64, _p],
     "aq_head_argmax_q6": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
     "aq_head_q6_candidates": [_i64, _i64],

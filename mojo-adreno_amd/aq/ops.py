@@ -168,9 +168,9 @@ def _t2_gemv_impl(x2h, w, s, y, workspace):
               workspace.numel() * workspace.element_size(), _stream(y))
 
 
-def t2_head_candidates(n: int) -> int:
-    """Argmax keys the ternary head leaves for an N-row vocabulary (one per workgroup)."""
-    return int(_lib.lib().aq_t2_head_candidates(n))
+def t2_head_candidates(n: int, k: int) -> int:
+    """Argmax keys the ternary head leaves for an N x K head (one per workgroup)."""
+    return int(_lib.lib().aq_t2_head_candidates(n, k))
 
 
 def _t2_head_argmax_impl(x2h, w, s, logits, cand, token, pos, hist, advance):

@@ -25,7 +25,8 @@ QWEN3_MOE = dict(experts=128, hidden=2048, ffn=768, topk=8, group=32)
 C3_TOKENS = 404
 
 
-LFM2_HEAD = dict(vocab=65536, hidden=2048)  # LFM2.5's tied Q6_K embedding / output head
+LFM2_HEAD = dict(vocab=128000, hidden=2048)  # LFM2.5's tied Q6_K embedding / output head (lfm2/README.md:116)
+BONSAI_HEAD = dict(vocab=248320, hidden=2048)  # Bonsai's ternary vocabulary head (bonsai/bonsai_vk.c:39)
 
 
 def q6_matrix(rng: np.random.Generator, rows: int, cols: int):

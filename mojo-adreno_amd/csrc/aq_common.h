@@ -102,6 +102,16 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)idx;
 }
+// Maximum of a 64-bit value over the wave, in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const uint64_t o = __shfl_xor(m, s, kWave);
+    m = o > m ? o : m;
+  }
+  return m;
+}
+
 // The key a producer leaves when any of its values is not finite: above every key of a finite value, so the step's
 // maximum is this key exactly when some logit was NaN or infinite (the token is then -1).
 constexpr uint64_t kNonFiniteKey = ~0ull;

@@ -93,13 +93,7 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // The first maximum among the lanes' (value, row) pairs (row < 0: none) as an argmax key, in every lane.
 __device__ __forceinline__ uint64_t wave_key_max(float best, int best_row) {
-  uint64_t m = best_row < 0 ? 0ull : argmax_key(best, best_row);
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    const uint64_t o = __shfl_xor(m, s, kWave);
-    m = o > m ? o : m;
-  }
-  return m;
+  return wave_max_u64(best_row < 0 ? 0ull : argmax_key(best, best_row));
 }
 
 struct Q6Args {

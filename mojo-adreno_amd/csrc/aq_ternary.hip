@@ -37,6 +37,79 @@ __device__ __forceinline__ float t2_word_dot(uint32_t w, const uint32_t* xp, flo
   return acc;
 }
 
+// t2_word_dot with the fp16-pair exponent bits 0x64006400 passed in a VGPR (magic), so each mask-and-OR is one
+// v_and_or_b32 instead of an AND and an OR with a literal.
+__device__ __forceinline__ float t2_word_dot_m(uint32_t w, const uint32_t* xp, float acc, uint32_t magic) {
+  const uint32_t hi = w >> 10;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = j <= 4 ? j : j - 5;
+    const uint32_t bits = ((j <= 4 ? w : hi) & (0x00030003u << (2 * e))) | magic;
+    const _Float16 bias = (_Float16)(1024.0f + (float)(1 << (2 * e)));
+    const half2v h = __builtin_bit_cast(half2v, bits) - half2v{bias, bias};
+    acc = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc, false);
+  }
+  return acc;
+}
+
+// Biased decode (the faster form; gfx950 issues v_bitop3_b32 and shifts at twice the rate of v_and_or_b32 and
+// v_pk_add_f16). The word is shifted so that code positions p = 2i, 2i + 1 (i < 4) land at bits 6-7 and 8-9 of both
+// halves (w << 6, << 2, >> 2, >> 6); one v_bitop3 per pair keeps those bits and fills the rest from 0x4C00 (16.0) or
+// 0x4400 (4.0), giving the exact fp16 pair (16 + c, 16 + c') for even p and (4 + c, 4 + c') for odd p. Their
+// v_dot2_f32_f16 with the unscaled x pair (x[p], x[p + 8]) sums (B_k + c_k) x_k; the caller subtracts the staged bias
+// sum_k (B_k + 1) x_k (B_k = 16 for even k % 8, else 4), leaving sum_k (c_k - 1) x_k. 56 issue cycles per word
+// against 98 for t2_word_dot_m.
+__device__ __forceinline__ uint32_t t2_pick(uint32_t a, uint32_t magic, uint32_t mask) {
+  return __builtin_amdgcn_bitop3_b32(a, magic, mask, 0xE4);  // mask ? a : magic, bit by bit
+}
+
+__device__ __forceinline__ float t2_word_dot_b(uint32_t w, const uint32_t* xp, float acc, uint32_t m16, uint32_t m4) {
+  const uint32_t sh[4] = {w << 6, w << 2, w >> 2, w >> 6};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, t2_pick(sh[i], m16, 0x00C000C0u)),
+                                 __builtin_bit_cast(half2v, xp[2 * i]), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, t2_pick(sh[i], m4, 0x03000300u)),
+                                 __builtin_bit_cast(half2v, xp[2 * i + 1]), acc, false);
+  }
+  return acc;
+}
+
+// Weight of x_k in the biased decode's bias: B_k + 1 for pair position p = k % 8.
+__device__ __forceinline__ float t2_bias_weight(int p) { return (p & 1) ? 5.0f : 17.0f; }
+
+// One k-row's x pairs (x[16 r + p], x[16 r + p + 8]) from its 16 fp16 (xl: x[16 r .. + 8), xh: x[16 r + 8 .. + 16)),
+// and its share of the biased decode's bias, sum_p (B_p + 1) (x[16 r + p] + x[16 r + p + 8]).
+__device__ __forceinline__ float t2_row_pairs(uint4 xl, uint4 xh, uint32_t (&pr)[8]) {
+  const uint32_t lo[4] = {xl.x, xl.y, xl.z, xl.w}, hi[4] = {xh.x, xh.y, xh.z, xh.w};
+  float bias = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    pr[2 * m] = (lo[m] & 0xFFFFu) | (hi[m] << 16);
+    pr[2 * m + 1] = (lo[m] >> 16) | (hi[m] & 0xFFFF0000u);
+    bias = fmaf(t2_bias_weight(2 * m), half_bits_to_float((uint16_t)lo[m]) + half_bits_to_float((uint16_t)hi[m]),
+                bias);
+    bias = fmaf(t2_bias_weight(2 * m + 1),
+                half_bits_to_float((uint16_t)(lo[m] >> 16)) + half_bits_to_float((uint16_t)(hi[m] >> 16)), bias);
+  }
+  return bias;
+}
+
+// Stages x (X2H words, K/2 of them) for t2_word_dot_b: xs[8 r + p] = the pairs of k-row r, gbias[g] = the bias of
+// 128-group g. Thread t of nthreads (a multiple of 64) takes rows t, t + nthreads, ...; a group is 8 consecutive
+// rows, i.e. 8 consecutive threads, all staging or all idle (krows % 8 == 0), summed by DPP.
+__device__ __forceinline__ void t2_stage_x(const uint32_t* __restrict__ x2h, uint32_t* xs, float* gbias, int krows,
+                                           int t, int nthreads) {
+  for (int r = t; r < krows; r += nthreads) {
+    const uint4* row = reinterpret_cast<const uint4*>(x2h + r * 8);
+    uint32_t pr[8];
+    const float bias = sum8(t2_row_pairs(row[0], row[1], pr));
+    *reinterpret_cast<uint4*>(xs + r * 8) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    *reinterpret_cast<uint4*>(xs + r * 8 + 4) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+    if ((r & 7) == 0) gbias[r >> 3] = bias;
+  }
+}
+
 // The reference's split interface (packed_linear): workgroup (column tile ct, split sp) covers columns [256 ct, +256)
 // (lane l -> columns 4l..4l+3, all four waves) and k-rows [sp * krows_wg, +krows_wg) (1024 k), divided among the four
 // waves in whole 128-groups, and writes partial[sp][n].
@@ -129,25 +202,19 @@ __global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict_
 // Fused ternary GEMV without any cross-workgroup step. A 512-thread workgroup owns CB consecutive columns over all
 // of K: lane l takes column l % CB and phase l / CB of its wave; the 8 * 64 / CB phases split the k-rows into
 // contiguous runs of whole 128-groups, so a load instruction reads CB consecutive words of 64/CB rows. Phase partials
-// are summed in phase order through LDS (deterministic). x' (scaled fp16 pairs) is staged in LDS once.
+// are summed in phase order through LDS (deterministic). x pairs and the per-group biases of t2_word_dot_b are
+// staged in LDS once.
 template <int CB>
 // cand != NULL: the workgroup also leaves the argmax key of its CB outputs (first maximum) in cand[blockIdx.x].
 __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
                                                       int K, uint64_t* __restrict__ cand) {
   constexpr int PH = 8 * 64 / CB;  // phases per workgroup
-  extern __shared__ uint32_t xs[];   // [K/16][8] scaled x pairs
+  extern __shared__ uint32_t xs[];   // [K/16][8] x pairs (x[16 r + p], x[16 r + p + 8]), then [K/128] group biases
   __shared__ float red[PH][CB];
   const int krows = K >> 4;
-  for (int i = threadIdx.x; i < krows * 8; i += 512) {
-    const int r = i >> 3, j = i & 7;
-    const int k = r * 16 + j;
-    const uint32_t lo = x2h[k >> 1], hi = x2h[(k + 8) >> 1];
-    const float a = half_bits_to_float((uint16_t)(k & 1 ? lo >> 16 : lo & 0xFFFF));
-    const float b = half_bits_to_float((uint16_t)((k + 8) & 1 ? hi >> 16 : hi & 0xFFFF));
-    const float f = t2_xscale(j);
-    xs[i] = (uint32_t)float_to_half_bits(a * f) | ((uint32_t)float_to_half_bits(b * f) << 16);
-  }
+  float* gbias = reinterpret_cast<float*>(xs + krows * 8);
+  t2_stage_x(x2h, xs, gbias, krows, threadIdx.x, 512);
   __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -160,8 +227,9 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
       const_cast<uint32_t*>(w), (short)0, (int)min((size_t)krows * N * 4, (size_t)0x7FFFFFFF), 0x00020000);
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(sc), (short)0,
                                                                        (int)((size_t)groups * N * 2), 0x00020000);
-  uint32_t magic;  // the fp16-pair exponent bits in a VGPR, so each mask-and-OR is one v_and_or_b32
-  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  uint32_t m16, m4;  // the fp16-pair fill patterns in VGPRs (the masks take the one scalar operand)
+  asm volatile("v_mov_b32 %0, 0x4c004c00" : "=v"(m16));
+  asm volatile("v_mov_b32 %0, 0x44004400" : "=v"(m4));
   const bool col_ok = n < N;
   float tot = 0.f;
   for (int g = g0; g < g1; ++g) {
@@ -172,22 +240,14 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
                                                    0);
     const float s = half_bits_to_float(
         __builtin_amdgcn_raw_buffer_load_b16(srs, col_ok ? ((uint32_t)g * N + n) * 2 : 0x80000000u, 0, 0));
-    float acc0 = 0.f, acc1 = 0.f;
+    float acc0 = -gbias[g], acc1 = 0.f;  // two chains: even and odd rows
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const uint4 x0 = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8);
-      const uint4 x1 = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8 + 4);
-      const uint32_t xp[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      const uint32_t hi = wv[r] >> 10;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int e = j <= 4 ? j : j - 5;
-        const uint32_t bits = ((j <= 4 ? wv[r] : hi) & (0x00030003u << (2 * e))) | magic;
-        const _Float16 bias = (_Float16)(1024.0f + (float)(1 << (2 * e)));
-        const half2v h = __builtin_bit_cast(half2v, bits) - half2v{bias, bias};
-        if (j & 1) acc1 = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc1, false);
-        else acc0 = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(half2v, xp[j]), acc0, false);
-      }
+      uint32_t xp[8];
+      *reinterpret_cast<uint4*>(xp) = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8);
+      *reinterpret_cast<uint4*>(xp + 4) = *reinterpret_cast<const uint4*>(xs + (g * 8 + r) * 8 + 4);
+      if (r & 1) acc1 = t2_word_dot_b(wv[r], xp, acc1, m16, m4);
+      else acc0 = t2_word_dot_b(wv[r], xp, acc0, m16, m4);
     }
     tot = fmaf(acc0 + acc1, s, tot);
   }
@@ -212,6 +272,114 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
         bad |= !__builtin_isfinite(red[0][j]);
       }
       cand[blockIdx.x] = bad ? kNonFiniteKey : argmax_key(best, c0 + bi);
+    }
+  }
+}
+
+// Wide matrices (a vocabulary head: many columns, K <= 16384): a 256-thread workgroup owns 256 consecutive columns
+// over all of K (lane l: columns 4 l .. 4 l + 3, one 16-byte load per k-row); wave w takes the 128-groups w, w + 4,
+// ... Wave partials are summed in wave order through LDS. cand != NULL: the workgroup's argmax key (first maximum of
+// its columns; kNonFiniteKey if any of them is NaN or infinite) goes to cand[blockIdx.x]. N % 4 == 0.
+__global__ __launch_bounds__(256) void k_t2_gemv_wide(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
+                                                      int K, uint64_t* __restrict__ cand) {
+  constexpr int CPL = 4, COLS = 256;
+  extern __shared__ uint32_t xs[];  // [K/16][8] x pairs (x[16 r + p], x[16 r + p + 8]), then [K/128] group biases
+  __shared__ float red[4][COLS];
+  __shared__ uint64_t kred[4];
+  const int krows = K >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float* gbias = reinterpret_cast<float*>(xs + krows * 8);
+  const int n0 = blockIdx.x * COLS + lane * CPL;
+  const bool ok = n0 < N;
+  const int groups = krows >> 3;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)krows * N * 4));
+  const auto sr = make_rsrc(sc, (uint32_t)((size_t)groups * N * 2));
+  auto issue = [&](int g, uint4 (&wv)[8], uint32_t (&s)[2]) {
+    const bool v = ok && g < groups;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wv[r] = buf_load16(wr, v ? ((uint32_t)(g * 8 + r) * N + n0) * 4 : kOOB);
+    const uint2 t = __builtin_bit_cast(
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(sr, v ? ((uint32_t)g * N + n0) * 2 : kOOB, 0, 0));
+    s[0] = t.x, s[1] = t.y;
+  };
+  // x: thread r stages k-row r (two 16-byte loads of x2h: x[16 r .. 16 r + 8) and x[16 r + 8 .. 16 r + 16)); the
+  // first round's loads are issued before the weights, so waiting for them does not wait for the weights
+  const auto xr = make_rsrc(x2h, (uint32_t)K * 2);
+  uint4 xlo = buf_load16(xr, (int)threadIdx.x < krows ? threadIdx.x * 32 : kOOB);
+  uint4 xhi = buf_load16(xr, (int)threadIdx.x < krows ? threadIdx.x * 32 + 16 : kOOB);
+  // two register sets in turn (no copies, which would wait for the loads in flight), both filled before x is staged
+  // (the weights do not depend on it): one group's words are used while the next ones load. Both sets are used
+  // unconditionally (a condition would let the compiler move their loads down to their use); past the last group
+  // the loads return zero, and a zero scale adds nothing.
+  uint4 wa[8], wb[8];
+  uint32_t sa[2], sb[2];
+  issue(wave, wa, sa);
+  issue(wave + 4, wb, sb);
+  // row r's pairs (x[16 r + p], x[16 r + p + 8]) and its bias sum_p (B_p + 1) (x[16 r + p] + x[16 r + p + 8]); a
+  // 128-group is 8 consecutive rows, i.e. 8 consecutive threads, all staging or all idle (krows % 8 == 0). The
+  // first round runs on every thread (rows past the end loaded zeros and store nothing), so its loads stay ahead of
+  // the weights'.
+  auto stage = [&](int r, uint4 xl, uint4 xh) {
+    uint32_t pr[8];
+    float bias = t2_row_pairs(xl, xh, pr);
+    bias = sum8(bias);
+    if (r < krows) {
+      *reinterpret_cast<uint4*>(xs + r * 8) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+      *reinterpret_cast<uint4*>(xs + r * 8 + 4) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+      if ((r & 7) == 0) gbias[r >> 3] = bias;
+    }
+  };
+  stage(threadIdx.x, xlo, xhi);
+  for (int r = threadIdx.x + 256; r < krows; r += 256) stage(r, buf_load16(xr, r * 32), buf_load16(xr, r * 32 + 16));
+  __syncthreads();
+  uint32_t m16, m4;  // the fp16-pair fill patterns in VGPRs (the masks take the one scalar operand)
+  asm volatile("v_mov_b32 %0, 0x4c004c00" : "=v"(m16));
+  asm volatile("v_mov_b32 %0, 0x44004400" : "=v"(m4));
+  float tot[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) tot[c] = 0.f;
+  auto compute = [&](int g, const uint4 (&wv)[8], const uint32_t (&s)[2]) {
+    // past the last group (its loads returned zero, scale 0) any staged group's x keeps the sum finite
+    const int gx = g < groups ? g : 0;
+    const float b0 = -gbias[gx];
+    float acc[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[c] = b0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      uint32_t xp[8];
+      *reinterpret_cast<uint4*>(xp) = *reinterpret_cast<const uint4*>(xs + (gx * 8 + r) * 8);
+      *reinterpret_cast<uint4*>(xp + 4) = *reinterpret_cast<const uint4*>(xs + (gx * 8 + r) * 8 + 4);
+      const uint32_t* words = reinterpret_cast<const uint32_t*>(&wv[r]);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[c] = t2_word_dot_b(words[c], xp, acc[c], m16, m4);
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      tot[c] = fmaf(acc[c], half_bits_to_float((uint16_t)(s[c >> 1] >> (16 * (c & 1)))), tot[c]);
+  };
+  for (int g = wave; g < groups; g += 8) {
+    compute(g, wa, sa);
+    issue(g + 8, wa, sa);
+    compute(g + 4, wb, sb);
+    issue(g + 12, wb, sb);
+  }
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) red[wave][lane * CPL + c] = tot[c];
+  __syncthreads();
+  const int t = threadIdx.x, n = blockIdx.x * COLS + t;  // one column a thread
+  const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+  if (n < N) y[n] = v;
+  if (cand) {  // workgroup-uniform
+    const uint64_t key = n >= N ? 0ull : __builtin_isfinite(v) ? argmax_key(v, n) : kNonFiniteKey;
+    const uint64_t m = wave_max_u64(key);
+    if (lane == 0) kred[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t b = kred[0];
+      for (int i = 1; i < 4; ++i) b = kred[i] > b ? kred[i] : b;
+      cand[blockIdx.x] = b;
     }
   }
 }
@@ -311,14 +479,23 @@ extern "C" int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k) {
 }
 
 namespace aq {
-// 32-column blocks when that still gives >= 256 workgroups, else 16 (more workgroups, 64-byte segments)
-inline int t2_cols_per_block(int64_t n) { return (n + 31) / 32 >= 256 ? 32 : 16; }
+// Columns per workgroup: 256 (k_t2_gemv_wide) when that still gives >= 512 workgroups; else 32 (k_t2_gemv_cols)
+// when that gives >= 256, else 16 (more workgroups, 64-byte segments).
+inline int t2_cols_per_block(int64_t n, int64_t k) {
+  if (n % 4 == 0 && (n + 255) / 256 >= 512 && k <= 16384) return 256;
+  return (n + 31) / 32 >= 256 ? 32 : 16;
+}
 
 static int launch_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int N, int K,
                           uint64_t* cand, hipStream_t sm) {
-  const size_t lds = (size_t)(K / 16) * 8 * 4;  // x' staging: 8 scaled pairs per 16-k row = 2K bytes
+  // x staging: 8 pairs per 16-k row (2K bytes), then one bias per 128-group
+  const size_t lds = (size_t)(K / 16) * 8 * 4 + (size_t)(K / 128) * 4;
   if (lds > 64 * 1024) return AQ_ERR_CAPACITY;
-  if (t2_cols_per_block(N) == 32)
+  const int cb = t2_cols_per_block(N, K);
+  if (cb == 256)
+    hipLaunchKernelGGL(k_t2_gemv_wide, dim3((unsigned)((N + 255) / 256)), dim3(256), lds, sm, x2h, w, s, y, N, K,
+                       cand);
+  else if (cb == 32)
     hipLaunchKernelGGL(k_t2_gemv_cols<32>, dim3((unsigned)((N + 31) / 32)), dim3(512), lds, sm, x2h, w, s, y, N, K,
                        cand);
   else
@@ -338,8 +515,8 @@ extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t
   return launch_t2_gemv(x2h, w, s, y, (int)n, (int)k, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int64_t aq_t2_head_candidates(int64_t n) {
-  return n > 0 ? (n + aq::t2_cols_per_block(n) - 1) / aq::t2_cols_per_block(n) : 0;
+extern "C" int64_t aq_t2_head_candidates(int64_t n, int64_t k) {
+  return n > 0 ? (n + aq::t2_cols_per_block(n, k) - 1) / aq::t2_cols_per_block(n, k) : 0;
 }
 
 extern "C" int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* logits, int64_t n,
@@ -349,7 +526,7 @@ extern "C" int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const u
   if (st) return st;
   if (!logits || !cand || !token || !pos) return AQ_ERR_NULL;
   if (hist_cap < 0) return AQ_ERR_SHAPE;
-  const int64_t ncand = aq_t2_head_candidates(n);
+  const int64_t ncand = aq_t2_head_candidates(n, k);
   if (cand_cap < ncand) return AQ_ERR_CAPACITY;
   if (!aligned(cand, 8)) return AQ_ERR_ALIGN;
   hipStream_t sm = reinterpret_cast<hipStream_t>(stream);

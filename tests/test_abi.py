@@ -115,12 +115,15 @@ def test_t2_head_argmax_validation():
     lib = aq.lib()
     buf = ctypes.create_string_buffer(4096 + 16)
     p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
-    # one argmax key per workgroup: 32 columns each once that gives >= 256 workgroups, else 16
-    assert lib.aq_t2_head_candidates(151669) == 4740
-    assert lib.aq_t2_head_candidates(8000) == 500
-    assert lib.aq_t2_head_candidates(8192) == 256
-    assert lib.aq_t2_head_candidates(7) == 1
-    assert lib.aq_t2_head_candidates(0) == 0
+    # one argmax key per workgroup: 256 columns each when N % 4 == 0 gives >= 512 workgroups (K <= 16384), else 32
+    # once that gives >= 256 workgroups, else 16
+    assert lib.aq_t2_head_candidates(248320, 2048) == 970
+    assert lib.aq_t2_head_candidates(248320, 32768) == 7760
+    assert lib.aq_t2_head_candidates(151669, 2048) == 4740
+    assert lib.aq_t2_head_candidates(8000, 1024) == 500
+    assert lib.aq_t2_head_candidates(8192, 512) == 256
+    assert lib.aq_t2_head_candidates(7, 128) == 1
+    assert lib.aq_t2_head_candidates(0, 128) == 0
     assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 499, p, p, None, 0, 1, None) == 6   # too few keys
     assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 500, p, None, None, 0, 1, None) == 5  # no pos
     assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p + 4, 500, p, p, None, 0, 1, None) == 3  # misaligned keys

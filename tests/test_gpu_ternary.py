@@ -32,7 +32,7 @@ def _exact(codes, s, x):
 
 
 @pytest.mark.parametrize("n,k", [(256, 512), (12288, 4096), (4096, 12288), (300, 1024), (6, 128), (1000, 2176),
-                                 (37, 640)])
+                                 (37, 640), (131072, 512), (131076, 384)])
 def test_t2_gemv_kat_bit_exact(dev, n, k):
     import torch
     rng = np.random.default_rng(n + k)
@@ -166,9 +166,9 @@ def test_gemm_t2_add(dev):
 
 def _head(dev, codes, s, x, hist_len=16, pos0=5):
     import torch
-    n = codes.shape[0]
+    n, k = codes.shape
     logits = torch.empty(n, dtype=torch.float32, device=dev)
-    cand = torch.zeros(_ops().t2_head_candidates(n), dtype=torch.int64, device=dev)
+    cand = torch.zeros(_ops().t2_head_candidates(n, k), dtype=torch.int64, device=dev)
     tok = torch.full((1,), -7, dtype=torch.int32, device=dev)
     pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
     hist = torch.full((hist_len,), -9, dtype=torch.int32, device=dev)
@@ -177,7 +177,7 @@ def _head(dev, codes, s, x, hist_len=16, pos0=5):
     return to_np(logits), int(tok.item()), int(pos.item()), to_np(hist)
 
 
-@pytest.mark.parametrize("n,k", [(151669, 256), (8000, 1024), (8192, 512), (7, 128)])
+@pytest.mark.parametrize("n,k", [(151669, 256), (248320, 256), (8000, 1024), (8192, 512), (7, 128)])
 def test_t2_head_argmax_kat(dev, n, k):
     """Integer-exact logits, so the token must be the first maximum of the exact products (the reference's greedy()
     over packed_head candidates)."""
@@ -190,12 +190,14 @@ def test_t2_head_argmax_kat(dev, n, k):
     assert hist[5] == tok and (np.delete(hist, 5) == -9).all()
 
 
-def test_t2_head_argmax_ties_pick_the_first(dev):
-    """Columns 3, 40, 900 and 7000 are all +1 codes, the largest product: the token is 3, across workgroups."""
+@pytest.mark.parametrize("n", [8000, 248320])
+def test_t2_head_argmax_ties_pick_the_first(dev, n):
+    """Columns 3, 40, 900 and 7000 (and 140000) are all +1 codes, the largest product: the token is 3, across
+    workgroups."""
     rng = np.random.default_rng(3)
-    n, k = 8000, 256
+    k = 256
     codes = rng.integers(0, 3, size=(n, k))
-    codes[[3, 40, 900, 7000]] = 2
+    codes[[3, 40, 900, 7000] + ([140000] if n > 140000 else [])] = 2
     s = np.ones((k // 128, n), np.float16)
     x = np.ones(k, np.float32)
     lg, tok, pos, _ = _head(dev, codes, s, x)
@@ -204,11 +206,12 @@ def test_t2_head_argmax_ties_pick_the_first(dev):
 
 
 @pytest.mark.parametrize("bad", ["inf", "nan"])
-def test_t2_head_argmax_nonfinite_gives_minus_one(dev, bad):
+@pytest.mark.parametrize("n", [8000, 131072])
+def test_t2_head_argmax_nonfinite_gives_minus_one(dev, bad, n):
     """A NaN or infinite logit (here from an infinite or NaN scale of column 4321) yields token -1, where the
     reference's greedy() stops with "nonfinite logits"; the position still advances."""
     rng = np.random.default_rng(4)
-    n, k = 8000, 256
+    k = 256
     codes, s, x = _kat(rng, n, k)
     codes[4321] = 2
     s[:, 4321] = np.float16(bad)
@@ -217,17 +220,18 @@ def test_t2_head_argmax_nonfinite_gives_minus_one(dev, bad):
     assert tok == -1 and pos == 6 and hist[5] == -1
 
 
-def test_t2_head_argmax_float_logits(dev):
+@pytest.mark.parametrize("wide", ["cols", "wide"])
+def test_t2_head_argmax_float_logits(dev, wide):
     """Random ternary head with fp16 activations: logits vs the oracle, token = first maximum of the GPU logits."""
     import torch
     from aq import synth
     rng = np.random.default_rng(6)
-    n, k = 20000, 2048
+    n, k = (20000, 2048) if wide == "cols" else (131072, 1024)
     w, s = synth.ternary_matrix(rng, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     xh = orc.x2h_pack(x)
     logits = torch.empty(n, dtype=torch.float32, device=dev)
-    cand = torch.zeros(_ops().t2_head_candidates(n), dtype=torch.int64, device=dev)
+    cand = torch.zeros(_ops().t2_head_candidates(n, k), dtype=torch.int64, device=dev)
     tok = torch.zeros(1, dtype=torch.int32, device=dev)
     pos = torch.zeros(1, dtype=torch.int32, device=dev)
     torch.ops.aq.t2_head_argmax(to_dev(xh, dev), to_dev(w, dev), to_dev(s, dev), logits, cand, tok, pos,
