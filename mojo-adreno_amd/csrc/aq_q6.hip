@@ -19,7 +19,7 @@ namespace aq {
 namespace {
 
 constexpr int kQ6Bytes = 208;   // bytes of a super-block in q
-constexpr int kQ6Waves = 2048;  // waves of a head launch at most (each strides over the row groups)
+constexpr int kQ6Waves = 3072;  // waves of a head launch at most: 3 a SIMD (each strides over the row groups)
 static_assert(kQ6Waves <= AQ_HEAD_CANDIDATES, "one argmax key per wave");
 
 struct Q6Raw {
@@ -108,7 +108,7 @@ struct Q6Args {
 };
 
 // K <= 4096: UP lanes per row (the unit count rounded up to a power of two), 64 / UP rows a step, x in registers;
-// the next step's loads are issued before the current step's arithmetic.
+// the next three steps' loads are in flight during a step's arithmetic.
 template <int UP>
 __global__ __launch_bounds__(256) void k_head_q6(Q6Args a) {
   constexpr int RPW = 64 / UP;
@@ -159,18 +159,29 @@ __global__ __launch_bounds__(256) void k_head_q6(Q6Args a) {
   };
   float best = 0.f;
   int best_row = -1;
-  Q6Raw cur, nxt;
-  issue(wave, cur);
-  for (int rg = wave; rg < groups; rg += waves) {
-    issue(rg + waves, nxt);
-    const float v = group_sum<UP>(q6_dot(cur, xa, xb, sx, g)) * rs;
+  auto process = [&](int rg, const Q6Raw& r) {
+    const float v = group_sum<UP>(q6_dot(r, xa, xb, sx, g)) * rs;
     const int row = rg * RPW + sub;
     if (u == UP - 1 && row < a.rows) {
       a.y[row] = v;
       // rows arrive in ascending order, so `>` keeps the first maximum; NaN never wins
       if (!__builtin_isnan(v) && (best_row < 0 || v > best)) best = v, best_row = row;
     }
-    cur = nxt;
+  };
+  // three register sets in turn, all in flight ahead of their use (a copy from one to another would wait for the
+  // loads): a step's loads are issued three steps before its arithmetic. Every set is processed unconditionally so
+  // that its loads stay where they are issued; past the last row group they returned zero and nothing is stored.
+  Q6Raw ra, rb, rc;
+  issue(wave, ra);
+  issue(wave + waves, rb);
+  issue(wave + 2 * waves, rc);
+  for (int rg = wave; rg < groups; rg += 3 * waves) {
+    process(rg, ra);
+    issue(rg + 3 * waves, ra);
+    process(rg + waves, rb);
+    issue(rg + 4 * waves, rb);
+    process(rg + 2 * waves, rc);
+    issue(rg + 5 * waves, rc);
   }
   if (a.cand) {
     const uint64_t m = wave_key_max(best, best_row);
