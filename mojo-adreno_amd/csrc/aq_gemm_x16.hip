@@ -64,8 +64,12 @@ __device__ __forceinline__ half8 dequant_t2_natural(uint32_t w, int h, uint32_t 
 
 // FMT kQ4: Q4W rows [N, K/8] with fp16 scales [N, K/group]; kT2: T2W words [K/16, N] with scales [K/128, N] (dense
 // mode only). T2W is column-contiguous, so its loads are coalesced in the MFMA B layout directly (no ds_bpermute).
-template <int FMT, int MB, int NB, bool ADD, bool SPLIT, int MODE>
-__global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
+// W8: 512 threads, two groups of four waves run the same tile over the two halves of the workgroup's super-steps
+// (each with its own pair of X buffers), and their accumulators are summed through LDS at the end. A SIMD then holds
+// two waves, so one wave's dequantisation issues while the other's MFMAs run: with one wave per SIMD in-order issue
+// leaves most of the VALU work outside the MFMA shadow. The caller gives W8 an even number of super-steps.
+template <int FMT, int MB, int NB, bool ADD, bool SPLIT, int MODE, bool W8>
+__global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   const uint32_t* __restrict__ wq = ga.w;
   const uint16_t* __restrict__ ws = ga.s;
   const int M = ga.M, N = ga.N, K = ga.K, group = ga.group;
@@ -73,16 +77,23 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
   constexpr int NW = 16 * NB;
   constexpr int FR = MB * 4 * 64;  // uint4 slots per buffer: MB row blocks x 4 steps x 64 lanes
   static_assert(NB == 4, "the W prefetch issues one column block per MFMA step");
-  __shared__ uint4 xa[FR];
-  __shared__ uint4 xb[FR];
+  __shared__ uint4 xbuf[(W8 ? 4 : 2) * FR];
 
   int sp = 0, nt, m0, expert = 0;
   if (!tile_of<MODE>(ga, BM, sp, nt, m0, expert)) return;
   const int nsup = (K + kSuper - 1) / kSuper;
-  const int ks0 = sp * ga.sup_per_split;
-  const int ks1 = min(nsup, ks0 + ga.sup_per_split);
+  int ks0 = sp * ga.sup_per_split;
+  int ks1 = min(nsup, ks0 + ga.sup_per_split);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int grp = W8 ? (int)(threadIdx.x >> 8) : 0;  // the half of the super-steps this wave's group takes
+  const int wave = (threadIdx.x >> 6) & 3;             // the wave within its group of four
+  if constexpr (W8) {
+    const int half = (ks1 - ks0) >> 1;
+    ks0 += grp * half;
+    ks1 = ks0 + half;
+  }
+  uint4* const xa = xbuf + 2 * grp * FR;
+  uint4* const xb = xa + FR;
   const int nw0 = MODE == kGroupedSwiglu ? nt * (2 * NW) + wave * (NW / 2) : nt * (4 * NW) + wave * NW;
   const int kw = K >> 3;
   const int gpr = K / group;
@@ -242,40 +253,68 @@ __global__ __launch_bounds__(256) void k_gemm_x16(GemmArgs ga) {
     if (ks + 4 < ks1) step(xa, xb, w1, w0, ks + 4);
     if (ks + 5 < ks1) step(xb, xa, w2, w1, ks + 5);
   }
+  if constexpr (W8) {
+    // the last step's barrier follows its wait for the X loads: LDS is quiescent and no wave reads it any more
+    float4v* red = reinterpret_cast<float4v*>(xbuf);  // 4 * FR slots = 4 waves x MB x NB x 64 lanes
+    if (grp == 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red[((wave * MB + mb) * NB + nb) * 64 + lane] = acc[mb][nb];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] += red[((wave * MB + mb) * NB + nb) * 64 + lane];
+  }
   gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
 }
 
-template <int FMT, int MB, int MODE>
+template <int FMT, int MB, int MODE, bool W8>
 static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
   constexpr int NB = 4;
+  const dim3 block(W8 ? 512 : 256);
   if constexpr (MODE == kDense) {
-    if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE>), dim3(blocks), dim3(256), 0, s, ga);
-    else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
-    else hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE, W8>), dim3(blocks), block, 0, s, ga);
+    else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
+    else hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
   } else {
-    hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE>), dim3(blocks), dim3(256), 0, s, ga);
+    hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
   }
 }
 
-template <int FMT, int MODE>
+template <int FMT, int MODE, bool W8>
 static void launch_mode(const GemmArgs& ga, int mb, bool add, bool split, int blocks, hipStream_t s) {
   switch (mb) {
-    case 1: return launch_mb<FMT, 1, MODE>(ga, add, split, blocks, s);
-    case 2: return launch_mb<FMT, 2, MODE>(ga, add, split, blocks, s);
-    case 3: return launch_mb<FMT, 3, MODE>(ga, add, split, blocks, s);
-    case 4: return launch_mb<FMT, 4, MODE>(ga, add, split, blocks, s);
-    case 5: return launch_mb<FMT, 5, MODE>(ga, add, split, blocks, s);
-    case 6: return launch_mb<FMT, 6, MODE>(ga, add, split, blocks, s);
-    default: return launch_mb<FMT, 7, MODE>(ga, add, split, blocks, s);
+    case 1: return launch_mb<FMT, 1, MODE, W8>(ga, add, split, blocks, s);
+    case 2: return launch_mb<FMT, 2, MODE, W8>(ga, add, split, blocks, s);
+    case 3: return launch_mb<FMT, 3, MODE, W8>(ga, add, split, blocks, s);
+    case 4: return launch_mb<FMT, 4, MODE, W8>(ga, add, split, blocks, s);
+    case 5: return launch_mb<FMT, 5, MODE, W8>(ga, add, split, blocks, s);
+    case 6: return launch_mb<FMT, 6, MODE, W8>(ga, add, split, blocks, s);
+    default: return launch_mb<FMT, 7, MODE, W8>(ga, add, split, blocks, s);
   }
 }
 
-// Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok.
+template <bool W8>
+static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
+  if (fmt == kT2) launch_mode<kT2, kDense, W8>(ga, mb, add, split, blocks, s);
+  else if (mode == kDense) launch_mode<kQ4, kDense, W8>(ga, mb, add, split, blocks, s);
+  else if (mode == kGrouped) launch_mode<kQ4, kGrouped, W8>(ga, mb, false, false, blocks, s);
+  else launch_mode<kQ4, kGroupedSwiglu, W8>(ga, mb, false, false, blocks, s);
+}
+
+// Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok. Every
+// workgroup's super-step range has the same even length when sup_per_split is even and divides the super-step count.
+// The 8-wave form runs for ranges of >= 16 super-steps (measured: C2's ternary GEMM 693 -> 769 TFLOP/s, C1's int4
+// gate|up unchanged; with 2-8 super-steps a group, C1's split-K projections lose 5-10%).
 int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
-  if (fmt == kT2) launch_mode<kT2, kDense>(ga, mb, add, split, blocks, s);
-  else if (mode == kDense) launch_mode<kQ4, kDense>(ga, mb, add, split, blocks, s);
-  else if (mode == kGrouped) launch_mode<kQ4, kGrouped>(ga, mb, false, false, blocks, s);
-  else launch_mode<kQ4, kGroupedSwiglu>(ga, mb, false, false, blocks, s);
+  const int nsup = (ga.K + kSuper - 1) / kSuper;
+  const int per = mode == kDense ? ga.sup_per_split : nsup;
+  if (per >= 16 && per % 2 == 0 && nsup % per == 0) launch_fmt<true>(ga, fmt, mb, add, split, mode, blocks, s);
+  else launch_fmt<false>(ga, fmt, mb, add, split, mode, blocks, s);
   return launch_status();
 }
 
