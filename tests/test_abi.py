@@ -137,8 +137,9 @@ def test_q6_validation():
     buf = ctypes.create_string_buffer(4096 + 16)
     p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
     f = ctypes.c_float(1e-5)
-    # one argmax key per wave: 65536 rows x 2048 (2 rows a wave step) -> 2048 waves; 7 rows x 256 (16 a step) -> 4
-    assert lib.aq_head_q6_candidates(65536, 2048) == 2048
+    # one argmax key per wave, at most 3072 waves: 65536 rows x 2048 (2 rows a wave step) -> 3072; 7 rows x 256
+    # (16 a step) -> 4
+    assert lib.aq_head_q6_candidates(65536, 2048) == 3072
     assert lib.aq_head_q6_candidates(7, 256) == 4
     assert lib.aq_head_q6_candidates(1000, 5120) == 1000
     assert lib.aq_head_q6_candidates(10, 100) == 0
@@ -146,7 +147,7 @@ def test_q6_validation():
     assert lib.aq_gemv_q6(p + 8, p, p, p, 100, 2048, None) == 3          # q not 16-byte aligned
     assert lib.aq_gemv_q6(p, p, None, p, 100, 2048, None) == 5
     assert lib.aq_gemv_q6(p, p, p, p, 1 << 24, 2048, None) == 6          # q beyond 2 GiB
-    assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 2047, p, p, None, 0, 1, None) == 6
+    assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 3071, p, p, None, 0, 1, None) == 6
     assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p + 4, 4096, p, p, None, 0, 1, None) == 3
     assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 4096, p, None, None, 0, 1, None) == 5
     assert lib.aq_embed_q6(p, p, 100, 2048, p, 0, p, None) == 1            # no tokens
