@@ -176,7 +176,7 @@ def bench_gemm_c1(dev, steps: int, warmup: int, layers: int = 16):
                 weights_mb=round(layers * sum(n * k * 0.5625 for _, n, k in C1_LAYER) / 1e6, 1))
 
 
-DOMINANT = "k_gemm_x16<7, 4, false, false, 0>"  # the fused gate|up launch of C1 (16384 x 2048, M = 431)
+DOMINANT = "k_gemm_x16<0, 7, 4, false, false, 0, true>"  # the fused gate|up launch of C1 (16384 x 2048, M = 431)
 DOMINANT_SHAPE = (431, 16384, 2048)
 
 

@@ -308,12 +308,14 @@ static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split
 
 // Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok. Every
 // workgroup's super-step range has the same even length when sup_per_split is even and divides the super-step count.
-// The 8-wave form runs for ranges of >= 16 super-steps (measured: C2's ternary GEMM 693 -> 769 TFLOP/s, C1's int4
-// gate|up unchanged; with 2-8 super-steps a group, C1's split-K projections lose 5-10%).
+// The 8-wave form runs for dense ranges of >= 16 super-steps (same-process A/B: C1's int4 gate|up 40.1 -> 37.8 us,
+// C2's ternary GEMM 5-12% faster; with 2-8 super-steps a group, C1's split-K projections lose 5-10%, and C3's
+// grouped gate|up goes from 84 to 94 us, so those keep four waves).
 int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
   const int nsup = (ga.K + kSuper - 1) / kSuper;
-  const int per = mode == kDense ? ga.sup_per_split : nsup;
-  if (per >= 16 && per % 2 == 0 && nsup % per == 0) launch_fmt<true>(ga, fmt, mb, add, split, mode, blocks, s);
+  const int per = ga.sup_per_split;
+  if (mode == kDense && per >= 16 && per % 2 == 0 && nsup % per == 0)
+    launch_fmt<true>(ga, fmt, mb, add, split, mode, blocks, s);
   else launch_fmt<false>(ga, fmt, mb, add, split, mode, blocks, s);
   return launch_status();
 }
