@@ -102,6 +102,13 @@ int aq_moe_gemm_q4(const void* x, int32_t x_is_f32, int64_t x_rows, const int32_
 int aq_moe_route(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts, int32_t topk,
                  void* stream);
 
+/* aq_moe_route, and with it x [tokens, d] fp32 rounded to fp16 pairs xq [tokens, d/2] (the grouped GEMM's input) in
+ * the same launch: one wave per token does both. d % 8 == 0, x and xq 16-byte aligned. Replaces: route / p_route
+ * (as aq_moe_route) followed by the fp32 -> fp16 rounding of the MoE block's input (lfm2moe/kernels/mk.mojo:164-176
+ * gathers fp32 rows; this build's grouped GEMM reads fp16). */
+int aq_moe_route_pack(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts,
+                      int32_t topk, const float* x, uint32_t* xq, int64_t d, void* stream);
+
 /* Grouping of the routed entries i = t*topk + k by expert (one workgroup, deterministic): counts[e]; offs[e] =
  * exclusive prefix sum of the counts padded to multiples of tm (offs[experts] = rows used); slot[i] = grouped row
  * (ascending i within an expert); src[row] = token (-1 on padding and unused rows < max_rows); work tiles (e, row)

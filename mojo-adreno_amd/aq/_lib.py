@@ -27,6 +27,7 @@ SIGNATURES: dict[str, list] = {
     "aq_gemm_t2_workspace_bytes": [_i64, _i64, _i64],
     "aq_moe_gemm_q4": [_p, _i32, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _i32, _i32, _i64, _i32, _p, _p],
     "aq_moe_route": [_p, _p, _p, _i64, _i32, _i32, _p],
+    "aq_moe_route_pack": [_p, _p, _p, _i64, _i32, _i32, _p, _p, _i64, _p],
     "aq_moe_group": [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
     "aq_moe_group_max_rows": [_i64, _i32, _i32, _i32],
     "aq_moe_group_max_tiles": [_i64, _i32, _i32, _i32],

@@ -48,7 +48,12 @@ class MoeBlock:
             raise ValueError(f"{t} tokens > max_tokens {self.max_tokens}")
         ids, wts = self.ids[:t], self.wts[:t]
         ops_ = torch.ops.aq
-        ops_.moe_route(logits, ids, wts, self.K)
+        if x.dtype == torch.float32 and x.shape[1] % 8 == 0:
+            # routing and one rounding of x to fp16 (instead of one per expert tile in the GEMM) in one launch
+            ops_.moe_route_pack(logits, ids, wts, self.K, x, self.xq[:t])
+            x = self.xq[:t].view(torch.float16)
+        else:
+            ops_.moe_route(logits, ids, wts, self.K)
         ops_.moe_group(ids, self.E, self.tm, self.counts, self.offs, self.slot[:t * self.K], self.src, self.tiles,
                        self.ntiles)
         if x.dtype == torch.float32:  # one rounding to fp16 here, instead of one per expert tile in the GEMM

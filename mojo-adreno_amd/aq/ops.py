@@ -295,6 +295,7 @@ def gemm_t2(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, y: torch.Tensor, 
 # ---- mixture of experts -------------------------------------------------------------------------------------------
 
 _LIB.define("moe_route(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk) -> ()")
+_LIB.define("moe_route_pack(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk, Tensor x, Tensor(c!) xq) -> ()")
 _LIB.define("moe_group(Tensor ids, int experts, int tm, Tensor(a!) counts, Tensor(b!) offs, Tensor(c!) slot, "
             "Tensor(d!) src, Tensor(e!) tiles, Tensor(f!) ntiles) -> ()")
 _LIB.define("moe_gemm_q4(Tensor x, Tensor src, Tensor wq, Tensor ws, int experts, int group, Tensor tiles, "
@@ -311,6 +312,20 @@ _LIB.define("moe_expert_lists(Tensor ids, int experts, Tensor(a!) lists, Tensor(
 def _i32(*ts):
     for t in ts:
         _check(t.dtype == torch.int32, "index tensors must be int32")
+
+
+def _moe_route_pack_impl(logits, ids, weights, topk, x, xq):
+    _dev(logits, ids, weights, x, xq)
+    _check(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be float32 [T, E]")
+    t, e = logits.shape
+    _check(ids.dtype == torch.int32 and ids.numel() == t * topk, "ids must be int32 [T, topk]")
+    _check(weights.dtype == torch.float32 and weights.numel() == t * topk, "weights must be float32 [T, topk]")
+    _check(x.dtype == torch.float32 and x.dim() == 2 and x.shape[0] == t, "x must be float32 [T, d]")
+    _u32(xq, "xq")
+    d = x.shape[1]
+    _check(xq.numel() * 2 == t * d, "xq must hold T * d / 2 words")
+    _lib.call("aq_moe_route_pack", _ptr(logits), _ptr(ids), _ptr(weights), t, e, topk, _ptr(x), _ptr(xq), d,
+              _stream(logits))
 
 
 def _moe_route_impl(logits, ids, weights, topk):
@@ -407,7 +422,7 @@ def _moe_expert_lists_impl(ids, experts, lists, counts, items_tt, items, nitems,
               items_ptr, items.numel() // 2, nitems_ptr, _ptr(scratch), scratch.numel(), _stream(ids))
 
 
-for _name, _fn in (("moe_route", _moe_route_impl), ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl),
+for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route_pack_impl), ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl),
                    ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
                    ("moe_down_q4", _moe_down_q4_impl), ("gemv_f32", _gemv_f32_impl),
                    ("moe_expert_lists", _moe_expert_lists_impl)):

@@ -11,60 +11,66 @@
 namespace aq {
 
 // ---- routing: top-k of E logits per token, lowest index among equals; weights = softmax over the k winners ----
-// One wave per token. The wave's logits go to LDS; each lane ranks its E/64 (<= 4) logits against all E of them
-// (broadcast reads): rank = #{greater} + #{equal with a lower index}, so ranks are distinct and rank r < k is the
-// r-th winner. The weights are exp(v_r - v_0) / sum_{r < k} exp(v_r - v_0), summed in rank order.
+// One wave per token, lane l holding logits l, l + 64, ... (PER_LANE of them). Round r: the wave maximum m of the
+// logits not yet taken (DPP), then the lowest index holding m among them (one ballot per slot: slot j's indices
+// 64 j .. 64 j + 63 are all below slot j + 1's), which is taken: the reference's iterated argmax (moek.mojo:164-186).
+// The weights are exp(v_r - v_0) / sum_{r < k} exp(v_r - v_0), summed in rank order. With xq, the wave also rounds
+// its token's row of x (d fp32, d % 8 == 0) to fp16 pairs for the grouped GEMM, issued first so the two overlap.
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int32_t* __restrict__ ids,
-                                               float* __restrict__ weights, int tokens, int E, int topk) {
-  __shared__ __align__(16) float lv[4][256];  // this wave's token's logits (E <= 256)
-  __shared__ float le[4][8];                  // exp(v_r - v_0) by rank
+                                               float* __restrict__ weights, int tokens, int E, int topk,
+                                               const float* __restrict__ x, uint32_t* __restrict__ xq, int d) {
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + w;
-  const bool active = t < tokens;  // no early return: every wave reaches the barriers
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;  // wave-uniform; the kernel has no barrier
+  if (xq) {
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * d);
+    uint4* qr = reinterpret_cast<uint4*>(xq + (size_t)t * (d / 2));
+    for (int i = lane; i < d / 8; i += 64) {
+      const float4 a = xr[2 * i], b = xr[2 * i + 1];
+      qr[i] = make_uint4((uint32_t)float_to_half_bits(a.x) | ((uint32_t)float_to_half_bits(a.y) << 16),
+                         (uint32_t)float_to_half_bits(a.z) | ((uint32_t)float_to_half_bits(a.w) << 16),
+                         (uint32_t)float_to_half_bits(b.x) | ((uint32_t)float_to_half_bits(b.y) << 16),
+                         (uint32_t)float_to_half_bits(b.z) | ((uint32_t)float_to_half_bits(b.w) << 16));
+    }
+  }
   float v[PER_LANE];
+  bool taken[PER_LANE];
 #pragma unroll
   for (int j = 0; j < PER_LANE; ++j) {
     const int e = lane + 64 * j;
-    v[j] = (active && e < E) ? logits[(size_t)t * E + e] : -INFINITY;
-    lv[w][e] = v[j];  // slots >= E hold -inf and are never counted
+    v[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
+    taken[j] = e >= E;  // padding slots are never candidates
   }
-  __syncthreads();
-  int rank[PER_LANE];
+  float top0 = 0.f, le = 0.f, total = 0.f;  // le: exp(v_r - v_0) of this lane's round r = lane
+  for (int r = 0; r < topk; ++r) {
+    float best = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < PER_LANE; ++j) rank[j] = 0;
-  // Slots E .. 64 * PER_LANE - 1 hold -inf: they are greater than no logit, and tie only with the -inf of lanes that
-  // hold no expert, which write nothing. So the scan runs over whole float4s without a bound check.
-  float vmax = -INFINITY;
-  const int e_end = (E + 3) & ~3;
-  for (int e2 = 0; e2 < e_end; e2 += 4) {
-    const float4 x4 = *reinterpret_cast<const float4*>(&lv[w][e2]);
-    const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+    for (int j = 0; j < PER_LANE; ++j) best = taken[j] ? best : fmaxf(best, v[j]);
+    const float m = wave_max(best);
+    int win = -1;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      vmax = fmaxf(vmax, xs[q]);
-#pragma unroll
-      for (int j = 0; j < PER_LANE; ++j)
-        rank[j] += (int)((xs[q] > v[j]) | ((xs[q] == v[j]) & (e2 + q < lane + 64 * j)));  // branch-free
+    for (int j = PER_LANE - 1; j >= 0; --j) {  // the lowest slot with a match decides
+      const uint64_t bal = __ballot(!taken[j] && v[j] == m);
+      if (bal) win = 64 * j + __builtin_ctzll(bal);
     }
-  }
+    if (win < 0) {  // no candidate equals m (NaN logits only): the lowest index not yet taken
 #pragma unroll
-  for (int j = 0; j < PER_LANE; ++j) {
-    const int e = lane + 64 * j;
-    if (active && e < E && rank[j] < topk) {
-      ids[(size_t)t * topk + rank[j]] = e;
-      le[w][rank[j]] = expf(v[j] - vmax);
+      for (int j = PER_LANE - 1; j >= 0; --j) {
+        const uint64_t bal = __ballot(!taken[j]);
+        if (bal) win = 64 * j + __builtin_ctzll(bal);
+      }
     }
-  }
-  __syncthreads();
-  float total = 0.f;
-  for (int r = 0; r < topk; ++r) total += le[w][r];
 #pragma unroll
-  for (int j = 0; j < PER_LANE; ++j) {
-    const int e = lane + 64 * j;
-    if (active && e < E && rank[j] < topk) weights[(size_t)t * topk + rank[j]] = le[w][rank[j]] / total;
+    for (int j = 0; j < PER_LANE; ++j)
+      if (lane + 64 * j == win) taken[j] = true;
+    if (r == 0) top0 = m;
+    const float ex = expf(m - top0);
+    total += ex;
+    if (lane == r) le = ex;
+    if (lane == 0) ids[(size_t)t * topk + r] = win;
   }
+  if (lane < topk) weights[(size_t)t * topk + lane] = le / total;
 }
 
 // ---- grouping: one 1024-thread workgroup --------------------------------------------------------------------------
@@ -234,19 +240,34 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ w, c
 
 using namespace aq;
 
+static int launch_route(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts,
+                        int32_t topk, const float* x, uint32_t* xq, int d, hipStream_t s) {
+  using namespace aq;
+  const dim3 grid((unsigned)((tokens + 3) / 4));
+  if (experts <= 64)
+    hipLaunchKernelGGL(k_route<1>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk, x, xq, d);
+  else if (experts <= 128)
+    hipLaunchKernelGGL(k_route<2>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk, x, xq, d);
+  else
+    hipLaunchKernelGGL(k_route<4>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk, x, xq, d);
+  return launch_status();
+}
+
 extern "C" int aq_moe_route(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts,
                             int32_t topk, void* stream) {
   if (!logits || !ids || !weights) return AQ_ERR_NULL;
   if (tokens <= 0 || experts <= 0 || experts > 256 || topk <= 0 || topk > 8 || topk > experts) return AQ_ERR_SHAPE;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)((tokens + 3) / 4));
-  if (experts <= 64)
-    hipLaunchKernelGGL(k_route<1>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
-  else if (experts <= 128)
-    hipLaunchKernelGGL(k_route<2>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
-  else
-    hipLaunchKernelGGL(k_route<4>, grid, dim3(256), 0, s, logits, ids, weights, (int)tokens, experts, topk);
-  return launch_status();
+  return launch_route(logits, ids, weights, tokens, experts, topk, nullptr, nullptr, 0,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int aq_moe_route_pack(const float* logits, int32_t* ids, float* weights, int64_t tokens, int32_t experts,
+                                 int32_t topk, const float* x, uint32_t* xq, int64_t d, void* stream) {
+  if (!logits || !ids || !weights || !x || !xq) return AQ_ERR_NULL;
+  if (tokens <= 0 || experts <= 0 || experts > 256 || topk <= 0 || topk > 8 || topk > experts) return AQ_ERR_SHAPE;
+  if (d <= 0 || d % 8 || tokens * d >= ((int64_t)1 << 31)) return AQ_ERR_SHAPE;
+  if (!aq::aligned(x, 16) || !aq::aligned(xq, 16)) return AQ_ERR_ALIGN;
+  return launch_route(logits, ids, weights, tokens, experts, topk, x, xq, (int)d, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t aq_moe_group_max_rows(int64_t tokens, int32_t topk, int32_t experts, int32_t tm) {

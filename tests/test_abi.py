@@ -152,3 +152,14 @@ def test_q6_validation():
     assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 4096, p, None, None, 0, 1, None) == 5
     assert lib.aq_embed_q6(p, p, 100, 2048, p, 0, p, None) == 1            # no tokens
     assert lib.aq_embed_q6(p, p, 100, 2048, None, 1, p, None) == 5
+
+
+def test_moe_route_pack_validation():
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    assert lib.aq_moe_route_pack(p, p, p, 4, 128, 8, None, p, 2048, None) == 5    # no x
+    assert lib.aq_moe_route_pack(p, p, p, 4, 128, 8, p, p, 2044, None) == 1       # d % 8
+    assert lib.aq_moe_route_pack(p, p, p, 4, 300, 8, p, p, 2048, None) == 1       # experts > 256
+    assert lib.aq_moe_route_pack(p, p, p, 4, 128, 8, p + 4, p, 2048, None) == 3   # x not 16-byte aligned

@@ -41,6 +41,45 @@ def test_route_ties_lowest_index(dev):
     np.testing.assert_array_equal(got, orc.route_top8(logits)[0])
 
 
+@pytest.mark.parametrize("t,e,k,d", [(404, 128, 8, 2048), (5, 256, 8, 64), (3, 64, 2, 8), (9, 33, 3, 24)])
+def test_route_pack(dev, t, e, k, d):
+    """The fused routing + fp16 rounding of x: ids and weights bit-equal to moe_route's, xq = fp16(x) (RNE)."""
+    import torch
+    rng = np.random.default_rng(t * 7 + d)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    x = (rng.standard_normal((t, d)) * 3).astype(np.float32)
+    x[0, :4] = [1e-8, 65504.0, -70000.0, 2.0 ** -24 * 1.5]  # fp16 subnormal, max, overflow, a rounding tie
+    ids = torch.empty((t, k), dtype=torch.int32, device=dev)
+    w = torch.empty((t, k), dtype=torch.float32, device=dev)
+    torch.ops.aq.moe_route(to_dev(logits, dev), ids, w, k)
+    ids2 = torch.empty_like(ids)
+    w2 = torch.empty_like(w)
+    xq = torch.empty((t, d // 2), dtype=torch.int32, device=dev)
+    torch.ops.aq.moe_route_pack(to_dev(logits, dev), ids2, w2, k, to_dev(x, dev), xq)
+    np.testing.assert_array_equal(to_np(ids2), to_np(ids))
+    np.testing.assert_array_equal(to_np(w2).view(np.uint32), to_np(w).view(np.uint32))
+    with np.errstate(over="ignore"):  # -70000 rounds to -inf in fp16, as intended
+        want = x.astype(np.float16)
+    np.testing.assert_array_equal(to_np(xq).view(np.uint16).reshape(t, d), want.view(np.uint16))
+
+
+def test_route_minus_infinity_logits(dev):
+    """-inf logits are ranked by index after the finite ones, none taken twice; their weights are 0."""
+    import torch
+    logits = np.full((2, 128), -np.inf, np.float32)
+    logits[0, [90, 7, 30]] = [0.5, 0.5, -1.0]
+    logits[1, :] = np.arange(128, dtype=np.float32)
+    logits[1, [1, 2]] = -np.inf
+    ids = torch.empty((2, 8), dtype=torch.int32, device=dev)
+    w = torch.empty((2, 8), dtype=torch.float32, device=dev)
+    torch.ops.aq.moe_route(to_dev(logits, dev), ids, w, 8)
+    rid, rw = orc.route_top8(logits, 8)
+    np.testing.assert_array_equal(to_np(ids), rid)
+    np.testing.assert_array_equal(to_np(ids)[0], [7, 90, 30, 0, 1, 2, 3, 4])
+    np.testing.assert_allclose(to_np(w), rw, rtol=2e-6, atol=1e-7)
+    assert (to_np(w)[0, 3:] == 0).all()
+
+
 @pytest.mark.parametrize("t,e,k,tm", [(404, 128, 8, 32), (404, 128, 8, 16), (50, 8, 2, 48), (1, 128, 8, 32),
                                       (1000, 128, 8, 64), (7, 3, 3, 16)])
 def test_group_bit_exact(dev, t, e, k, tm):
