@@ -476,12 +476,28 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     } else {
       for (int c = lane; c < nch; c += kWave) {
         if constexpr (MODE == kMoeDown) {
-          // one row per expert slot t, applied to that slot's activations only
+          // one row per expert slot t, applied to that slot's activations only. Every slot's 16 bytes (and scale)
+          // are requested before any is used (a slot with no expert reads zeros through an out-of-range offset), so
+          // the T loads are in flight together rather than one after another.
+          // the stacked experts' rows (the entry point keeps them below 2 GiB)
+          const uint32_t mrows = (uint32_t)moe.experts * (uint32_t)n_out;
+          const auto wm_rsrc = make_rsrc(wq, mrows * (uint32_t)kw * 4u);
+          const auto sm_rsrc = make_rsrc(ws, mrows * (uint32_t)gpr * 2u);
+          uint4 w4s[T];
+          uint32_t s4s[T];
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const int row = rows[0][t];
+            w4s[t] = buf_load16(wm_rsrc, row >= 0 ? ((uint32_t)row * (uint32_t)kw + (uint32_t)c * 4u) * 4u : kOOB);
+            if constexpr (G32)
+              s4s[t] = __builtin_amdgcn_raw_buffer_load_b16(
+                  sm_rsrc, row >= 0 ? ((uint32_t)row * (uint32_t)gpr + (uint32_t)((c * 32) >> gsh)) * 2u : kOOB, 0, 0);
+          }
 #pragma unroll
           for (int t = 0; t < T; ++t) {
             const int row = rows[0][t];
             if (row < 0) continue;  // wave-uniform
-            const uint4 w4 = *reinterpret_cast<const uint4*>(wq + (size_t)row * kw + c * 4);
+            const uint4 w4 = w4s[t];
             const uint32_t wv4[4] = {w4.x, w4.y, w4.z, w4.w};
             float part = 0.f;
             if constexpr (G32) {
@@ -500,7 +516,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
                 part = fmaf(dot8_biased(wv4[j], xv) - 8.0f * xsum[(t * 4 + j) * nch + c], sj, part);
               }
             }
-            if constexpr (G32) part *= half_bits_to_float(ws[(size_t)row * gpr + (c * 32) / group]);
+            if constexpr (G32) part *= half_bits_to_float((uint16_t)s4s[t]);
             acc[0][t] += part;
           }
         } else {  // a group smaller than 32 or not a multiple of it: one scale per 8-weight word
@@ -724,6 +740,7 @@ extern "C" int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t ex
                               int32_t topk, int32_t add, void* stream) {
   if (!ids || !weights) return AQ_ERR_NULL;
   if (topk <= 0 || topk > 8 || d <= 0 || experts <= 0 || experts * d > INT32_MAX) return AQ_ERR_SHAPE;
+  if (f > 0 && experts * d * (f / 2) >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;  // stacked W below 2 GiB
   // the expert slots are the kernel's "tokens": act [topk, f] holds one activation vector per slot
   const aq::MoeArgs moe{ids, weights, (int)experts, add ? 1 : 0};
   return aq::gemv_entry<aq::kMoeDown>(wq, ws, act, y, d, f, group, 0, topk, moe, stream);
