@@ -456,7 +456,7 @@ def main():
                          "the output heads")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+        print("bench.py measures one GPU: this build has no multi-GPU path (every kernel runs on one GPU's share)",
               file=sys.stderr)
         sys.exit(2)
     import torch
