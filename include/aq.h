@@ -311,6 +311,11 @@ int aq_gguf_q6_k_to_q6w(const uint8_t* blocks, int64_t rows, int64_t cols, uint8
  * sc = scales[8 h + 2 j + l / 16]. Replaces: q6_dequant + the "h6" recipe line of lfm2/convert.c:82-103,163-175. */
 int aq_gguf_q6_k_to_f16(const uint8_t* blocks, int64_t rows, int64_t cols, uint16_t* out);
 
+/* T2W scales from the (scale, bias) fp32 pairs [groups = K/128, n, 2] that bonsai/convert.cpp:44-61 (emitPacked)
+ * writes beside the transposed codes (those are T2W words already): s fp16 [groups, n] = the scales. Returns
+ * AQ_ERR_ARG, writing nothing, if any group is not ternary (bias != -scale) or a scale is not exact in fp16. */
+int aq_t2w_scales_from_pairs(const float* params, int64_t groups, int64_t n, uint16_t* s);
+
 /* MLX 2-bit projections -> one fused T2W matrix: part p has codes [rows[p], K/16], scales and biases fp16
  * [rows[p], K/128]; w [K/16, sum rows] (transposed), s [K/128, sum rows]. Returns AQ_ERR_ARG, writing nothing, if any
  * group is not ternary (bias != -scale). K % 128 == 0. Replaces: addPacked (qwen3/convert.cpp:39-74). */

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
     "aq_gguf_q4_0_to_q4w": [_p, _i64, _i64, _p, _p],
     "aq_gguf_q4_0_to_f16": [_p, _i64, _i64, _p],
     "aq_gguf_q6_k_to_q6w": [_p, _i64, _i64, _p, _p],
+    "aq_t2w_scales_from_pairs": [_p, _i64, _i64, _p],
     "aq_gguf_q6_k_to_f16": [_p, _i64, _i64, _p],
     "aq_t2w_from_mlx": [_p, _p, _p, _p, _i32, _i64, _p, _p],
 }

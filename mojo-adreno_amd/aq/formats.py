@@ -9,6 +9,7 @@ converters' bytes:
   gguf_q4_0_to_f16      lfm2/convert.c:73-80 "h4" (GGUF Q4_0 -> fp16)
   gguf_q6_k_to_q6w      lfm2/convert.c:148-155 "q6" (GGUF Q6_K -> 208-byte super-blocks + fp16 d apart)
   gguf_q6_k_to_f16      lfm2/convert.c:82-103 "h6" (GGUF Q6_K -> fp16)
+  t2w_scales_from_pairs bonsai/convert.cpp:44-61 emitPacked ((scale, bias) fp32 pairs -> T2W fp16 scales)
   t2w_from_mlx          qwen3/convert.cpp:39-74 addPacked (MLX 2-bit projections -> one transposed T2W matrix)
 
 Inputs are numpy arrays; bf16 weights are passed as their uint16 bit patterns (numpy has no bf16 type).
@@ -96,6 +97,17 @@ def gguf_q6_k_to_f16(blocks, rows: int, cols: int) -> np.ndarray:
     src = _q6_k_src(blocks, rows, cols)
     out = np.empty((rows, cols), np.float16)
     _lib.call("aq_gguf_q6_k_to_f16", _ptr(src), rows, cols, _ptr(out))
+    return out
+
+
+def t2w_scales_from_pairs(params: np.ndarray) -> np.ndarray:
+    """bonsai/convert.cpp's (scale, bias) pairs fp32 [K/128, N, 2] -> T2W scales fp16 [K/128, N]. Raises AqError if a
+    group is not ternary (bias != -scale) or a scale is not exact in fp16."""
+    src = np.ascontiguousarray(params, np.float32)
+    if src.ndim != 3 or src.shape[2] != 2:
+        raise ValueError("params must be [K/128, N, 2]")
+    out = np.empty(src.shape[:2], np.float16)
+    _lib.call("aq_t2w_scales_from_pairs", _ptr(src), src.shape[0], src.shape[1], _ptr(out))
     return out
 
 

@@ -10,6 +10,9 @@
 //   aq_gguf_q6_k_to_q6w      lfm2/convert.c "q6" (:148-155): GGUF Q6_K super-blocks (210 bytes: ql[128], qh[64],
 //                            int8 scales[16], fp16 d) -> their first 208 bytes [rows, cols/256, 208] and d apart.
 //   aq_gguf_q6_k_to_f16      lfm2/convert.c:82-103 q6_dequant + "h6": (d * sc) * (q - 32) in fp32, rounded to fp16.
+//   aq_t2w_scales_from_pairs bonsai/convert.cpp:44-61 emitPacked writes the codes already transposed (T2W words) and
+//                            fp32 (scale, bias) pairs [K/128, N, 2]; this keeps the fp16 scales [K/128, N] of a
+//                            ternary matrix (bias == -scale, the scale exact in fp16, as it came from fp16).
 //   aq_t2w_from_mlx          qwen3/convert.cpp:39-74 addPacked: MLX 2-bit codes [n_i, K/16] and scales/biases
 //                            [n_i, K/128] of several projections -> one transposed T2W matrix [K/16, sum n_i] and its
 //                            scales [K/128, sum n_i]; every group must be ternary (bias == -scale).
@@ -225,6 +228,18 @@ extern "C" int aq_gguf_q6_k_to_f16(const uint8_t* blocks, int64_t rows, int64_t 
           y[128 * h + 32 * j + l] = float_to_half(dd * (float)sc * (float)qv);
         }
   }
+  return AQ_OK;
+}
+
+extern "C" int aq_t2w_scales_from_pairs(const float* params, int64_t groups, int64_t n, uint16_t* s) {
+  if (!params || !s) return AQ_ERR_NULL;
+  if (groups <= 0 || n <= 0) return AQ_ERR_SHAPE;
+  const int64_t count = groups * n;
+  for (int64_t i = 0; i < count; ++i) {  // check everything first: nothing is written on an error
+    const float sc = params[2 * i], b = params[2 * i + 1];
+    if (b != -sc || half_to_float(float_to_half(sc)) != sc) return AQ_ERR_ARG;
+  }
+  for (int64_t i = 0; i < count; ++i) s[i] = float_to_half(params[2 * i]);
   return AQ_OK;
 }
 

@@ -550,6 +550,17 @@ def gemv_q6(q: np.ndarray, d: np.ndarray, x: np.ndarray) -> np.ndarray:
     return q6w_dequant(q, d).astype(np.float64) @ np.asarray(x, np.float64)
 
 
+def bonsai_pairs_to_t2w_scales(params: np.ndarray) -> np.ndarray:
+    """bonsai/convert.cpp:44-61 (``emitPacked``) stores each 128-group's fp16 scale and bias as an fp32 pair
+    [K/128, N, 2] next to the transposed codes; a ternary group has bias == -scale, and T2W keeps the scale in fp16
+    (exact: it came from fp16). ValueError for any other group."""
+    p = np.asarray(params, np.float32)
+    sc, b = p[..., 0], p[..., 1]
+    if np.any(b != -sc) or np.any(sc.astype(np.float16).astype(np.float32) != sc):
+        raise ValueError("not ternary, or a scale that fp16 does not hold")
+    return sc.astype(np.float16)
+
+
 def mlx_to_t2w(parts, k: int):
     """MLX 2-bit affine matrices -> one fused T2W matrix (qwen3/convert.cpp:39-74, ``addPacked``).
 

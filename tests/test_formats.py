@@ -152,3 +152,27 @@ def test_converter_errors(fmt):
         fmt.quantize_q4_searched(np.zeros((2, 1024), np.uint16), 512)  # group > 256
     assert _lib.lib().aq_gguf_q4_0_to_q4w(None, 1, 32, None, None) == 5  # AQ_ERR_NULL
     assert _lib.lib().aq_gguf_q4_0_to_f16(ctypes.c_void_p(8), 1, 33, ctypes.c_void_p(8)) == 1  # AQ_ERR_SHAPE
+
+
+def test_t2w_scales_from_bonsai_pairs(fmt):
+    """bonsai/convert.cpp's fp32 (scale, bias) pairs of a ternary matrix give back its fp16 scales exactly; a
+    non-ternary group, or a scale fp16 cannot hold, is refused and nothing is written."""
+    from aq import AqError
+    rng = np.random.default_rng(11)
+    s16 = (np.abs(rng.standard_normal((16, 300))) * 0.02).astype(np.float16)
+    s16[0, 0] = np.float16(6e-8)   # fp16 subnormal
+    s16[1, 1] = np.float16(0.0)
+    pairs = np.stack([s16.astype(np.float32), -s16.astype(np.float32)], axis=-1)
+    got = fmt.t2w_scales_from_pairs(pairs)
+    np.testing.assert_array_equal(_u16(got), _u16(s16))
+    np.testing.assert_array_equal(_u16(got), _u16(orc.bonsai_pairs_to_t2w_scales(pairs)))
+    bad = pairs.copy()
+    bad[3, 7, 1] += 1e-3           # bias != -scale: an affine 2-bit group
+    with pytest.raises(AqError):
+        fmt.t2w_scales_from_pairs(bad)
+    with pytest.raises(ValueError):
+        orc.bonsai_pairs_to_t2w_scales(bad)
+    bad = pairs.copy()
+    bad[2, 2] = [0.1, -0.1]        # 0.1 is not an fp16 value
+    with pytest.raises(AqError):
+        fmt.t2w_scales_from_pairs(bad)
