@@ -27,6 +27,8 @@ def _gemm(x, wq, ws, group, dev, add_to=None):
     (431, 512, 2048, 64, False), (200, 768, 1024, 128, False), (64, 256, 2048, 256, False),
     # scale rows that are not aligned for that load (K / group = 65, 33) take the general kernel
     (100, 256, 2080, 32, False), (90, 128, 2112, 64, False),
+    # tall tiles (M > 112, 128 columns): one row past a whole block, ragged columns, one super-step, three row tiles
+    (113, 130, 128, 32, False), (150, 200, 512, 32, False), (240, 1000, 384, 64, False), (700, 384, 256, 32, False),
 ])
 def test_kat_bit_exact(dev, m, n, k, group, xf32):
     """Integer-valued X, power-of-two scales: exact in fp16 and in fp32 accumulation, so the MFMA result must equal
@@ -50,6 +52,18 @@ def test_c1_projection_parity(dev, name):
     ref = orc.gemm_q4(wq, ws, x.astype(np.float32), 32)
     assert rel_inf(got, ref) < TOL_F16
     assert rel_l2(got, ref) < 2e-3
+
+
+def test_tall_tile_add(dev):
+    """The residual form on tall tiles (fp16 X, M > 112), with and without a split of K."""
+    rng = np.random.default_rng(31)
+    for m, n, k in ((300, 384, 1024), (431, 640, 8192)):
+        vals, ws, x = kat_int4(rng, n, k, 32, tokens=m)
+        x = x.astype(np.float16)
+        y0 = rng.integers(-4, 4, size=(m, n)).astype(np.float32)
+        got = _gemm(x, orc.q4w_pack(vals), ws, 32, dev, add_to=y0)
+        np.testing.assert_array_equal(got, (exact_int4_product(vals, ws, x.astype(np.float32), 32) + y0)
+                                      .astype(np.float32))
 
 
 def test_fp32_input_and_add(dev):

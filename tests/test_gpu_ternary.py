@@ -127,7 +127,7 @@ def _gemm_t2(x, w, s, dev, add_to=None):
 
 @pytest.mark.parametrize("m,n,k,xf32", [(16, 64, 128, False), (412, 256, 1024, False), (100, 300, 256, True),
                                         (412, 12288, 4096, False), (412, 4096, 12288, False), (1, 16, 128, False),
-                                        (33, 100, 640, True)])
+                                        (33, 100, 640, True), (113, 130, 128, False), (150, 200, 384, False)])
 def test_gemm_t2_kat_bit_exact(dev, m, n, k, xf32):
     """Integer-valued X and power-of-two scales: exact in fp16 MFMA with fp32 accumulation."""
     rng = np.random.default_rng(m + n + k)
@@ -153,15 +153,16 @@ def test_c2_gemm_parity(dev, name):
     assert rel_inf(got, orc.ternary_gemm(x.astype(np.float32), w, s)) < 1e-2
 
 
-def test_gemm_t2_add(dev):
+@pytest.mark.parametrize("m,xf32", [(64, True), (260, False)])
+def test_gemm_t2_add(dev, m, xf32):
     rng = np.random.default_rng(23)
-    n, k, m = 512, 1024, 64
+    n, k = 512, 1024
     from aq import synth
     w, s = synth.ternary_matrix(rng, n, k)
-    x = rng.standard_normal((m, k)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32 if xf32 else np.float16)
     y0 = rng.standard_normal((m, n)).astype(np.float32)
     got = _gemm_t2(x, w, s, dev, add_to=y0)
-    assert rel_inf(got, orc.ternary_gemm(x, w, s) + y0) < 1e-2
+    assert rel_inf(got, orc.ternary_gemm(x.astype(np.float32), w, s) + y0) < 1e-2
 
 
 def _head(dev, codes, s, x, hist_len=16, pos0=5):
