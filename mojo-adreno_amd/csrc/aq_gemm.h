@@ -113,6 +113,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& ga, const float4v (&a
 inline bool x16_shape_ok(int K, int group) {
   return K > 0 && K % 128 == 0 && group >= 32 && (group & (group - 1)) == 0;
 }
-int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s);
+// nb = 4: 256-column tiles (four or eight waves of 64 columns); nb = 2 (dense only): 128-column tiles.
+int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, int nb, bool add, bool split, int mode, int blocks,
+                    hipStream_t s);
 
 }  // namespace aq

@@ -15,6 +15,8 @@
 // is staged once per workgroup in LDS in fragment order with the same k permutation (halves 0,4,1,5,2,6,3,7 of each
 // 8-chunk), so a fragment is one ds_read_b128 per lane; slots are XOR-swizzled to keep staging writes 2-way. LDS is
 // double-buffered: the next super-step's X and W are fetched into registers while this one is multiplied.
+#include <algorithm>
+
 #include "aq_gemm.h"
 
 namespace aq {
@@ -299,26 +301,41 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 struct GemmPlan {
-  int mb, mtiles, ntiles, splits, sup_per_split;
+  int mb, nb, mtiles, ntiles, splits, sup_per_split;
 };
 
-// Rows per tile: the fewest 16-row blocks that cover M with ceil(M / 112) tiles (431 -> 4 x 112; at most 7 blocks,
-// so the accumulators and operands of a wave stay in 256 VGPRs). Splits of K: enough workgroups to cover the 256
-// CUs, each split keeping >= 2 super-steps of 128.
-constexpr int kMaxMB = 7;
-static GemmPlan plan_gemm(int M, int N, int K) {
+// Tiles of at most max_mb 16-row blocks (the fewest that cover M with that many tiles: 431 -> 4 x 112 at 7) and
+// `cols` columns; K split while the workgroups stay within `fill`, each split keeping >= 2 super-steps.
+constexpr int kMaxMB = 7;  // accumulators and operands of a wave stay in 256 VGPRs
+static GemmPlan plan_tiles(int M, int N, int K, int max_mb, int cols, int fill) {
   GemmPlan p;
   const int blocks16 = (M + 15) / 16;
-  p.mtiles = (blocks16 + kMaxMB - 1) / kMaxMB;
+  p.nb = cols / 64;
+  p.mtiles = (blocks16 + max_mb - 1) / max_mb;
   p.mb = (blocks16 + p.mtiles - 1) / p.mtiles;
-  p.ntiles = (N + 255) / 256;
+  p.ntiles = (N + cols - 1) / cols;
   const int nsup = (K + kSuper - 1) / kSuper;
   const int tiles = p.mtiles * p.ntiles;
   int s = 1;
-  while (tiles * s * 2 <= 320 && nsup / (s * 2) >= 2) s *= 2;
+  while (tiles * s * 2 <= fill && nsup / (s * 2) >= 2) s *= 2;
   p.sup_per_split = (nsup + s - 1) / s;
   p.splits = (nsup + p.sup_per_split - 1) / p.sup_per_split;
   return p;
+}
+
+// 256-column tiles of up to 112 rows, K split to cover the 256 CUs (up to 320 workgroups). For the direct-to-LDS
+// kernel (narrow_ok), shapes whose splits would hold only a few super-steps take 128-column tiles instead, which
+// need fewer splits (and fp32 partials): with <= 4 super-steps a split, tiles of 3 or 4 row blocks, whichever gives
+// more workgroups within one per CU; with <= 8, tiles of up to 7 blocks. Same-process A/B on MI355X at M = 431:
+// q|k|v (3072 x 2048) 23.4 -> 15.9 us (3 blocks, no split), o (2048 x 2048) 22.0 -> 16.2 (4 blocks, 2 splits),
+// down (2048 x 8192) 30.3 -> 28.3 (7 blocks, 4 splits). Longer splits lose: the ternary 4096 x 12288 at M = 412
+// went from 48 to 54 us with 7 blocks and 64 with 4.
+static GemmPlan plan_gemm(int M, int N, int K, bool narrow_ok) {
+  const GemmPlan p = plan_tiles(M, N, K, kMaxMB, 256, 320);
+  if (!narrow_ok || p.splits == 1 || p.sup_per_split > 8) return p;
+  if (p.sup_per_split > 4) return plan_tiles(M, N, K, kMaxMB, 128, 256);
+  const GemmPlan a = plan_tiles(M, N, K, 3, 128, 256), b = plan_tiles(M, N, K, 4, 128, 256);
+  return a.mtiles * a.ntiles * a.splits > b.mtiles * b.ntiles * b.splits ? a : b;
 }
 
 static int64_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
@@ -336,9 +353,9 @@ static int launch_gemm(const void* x, const uint32_t* wq, const uint16_t* ws, fl
   ga.M = M; ga.N = N; ga.K = K; ga.group = group; ga.mtiles = p.mtiles; ga.ntiles = p.ntiles;
   ga.splits = p.splits; ga.sup_per_split = p.sup_per_split;
   if constexpr (FMT == kQ4 && G32 && !XF32) {
-    if (x16_shape_ok(K, group)) return launch_gemm_x16(ga, kQ4, MB, ADD, SPLIT, kDense, blocks, s);
+    if (x16_shape_ok(K, group)) return launch_gemm_x16(ga, kQ4, MB, p.nb, ADD, SPLIT, kDense, blocks, s);
   }
-  if constexpr (FMT == kT2 && !XF32) return launch_gemm_x16(ga, kT2, MB, ADD, SPLIT, kDense, blocks, s);
+  if constexpr (FMT == kT2 && !XF32) return launch_gemm_x16(ga, kT2, MB, p.nb, ADD, SPLIT, kDense, blocks, s);
   const size_t lds = 2 * (size_t)MB * 256 * 16;
   auto kern = k_gemm<FMT, MB, NB, G32, XF32, ADD, SPLIT, kDense>;
   if (lds > 64 * 1024) {
@@ -395,14 +412,14 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
   if (!aligned(wq, 16) || !aligned(x, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int M = (int)m, N = (int)n, K = (int)k;
-  GemmPlan p = plan_gemm(M, N, K);
+  const bool g32 = FMT == kT2 || group % 32 == 0;
+  if (FMT == kT2) group = 128;
+  GemmPlan p = plan_gemm(M, N, K, !xf32 && g32 && x16_shape_ok(K, group));
   if (p.splits > 1 && (!workspace || ws_bytes < gemm_workspace_bytes(p, M, N) || !aligned(workspace, 16))) {
     p.splits = 1;  // no (or too small a) workspace: one pass over K
     p.sup_per_split = (K + kSuper - 1) / kSuper;
   }
   float* part = static_cast<float*>(workspace);
-  const bool g32 = FMT == kT2 || group % 32 == 0;
-  if (FMT == kT2) group = 128;
   if (xf32) return g32 ? gemm_dispatch<FMT, true, true>(x, wq, ws, y, part, M, N, K, group, add, p, s)
                        : gemm_dispatch<FMT, false, true>(x, wq, ws, y, part, M, N, K, group, add, p, s);
   return g32 ? gemm_dispatch<FMT, true, false>(x, wq, ws, y, part, M, N, K, group, add, p, s)
@@ -422,7 +439,7 @@ static int launch_grouped(const GemmArgs& ga0, int max_tiles, hipStream_t s) {
   const int blocks = ga.ntiles * max_tiles;
   if (blocks <= 0) return AQ_OK;
   if constexpr (G32 && !XF32) {
-    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, kQ4, MB, false, false, MODE, blocks, s);
+    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, kQ4, MB, 4, false, false, MODE, blocks, s);
   }
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();
@@ -499,8 +516,9 @@ extern "C" int aq_gemm_t2(const void* x, int32_t x_is_f32, const uint32_t* w, co
 extern "C" int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k);
 extern "C" int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return 0;
-  const aq::GemmPlan p = aq::plan_gemm((int)m, (int)n, (int)k);
-  return aq::gemm_workspace_bytes(p, (int)m, (int)n);
+  // the larger of the two tilings' needs: which one runs depends on X's type and the group
+  const aq::GemmPlan a = aq::plan_gemm((int)m, (int)n, (int)k, false), b = aq::plan_gemm((int)m, (int)n, (int)k, true);
+  return std::max(aq::gemm_workspace_bytes(a, (int)m, (int)n), aq::gemm_workspace_bytes(b, (int)m, (int)n));
 }
 
 extern "C" int64_t aq_gemm_t2_workspace_bytes(int64_t m, int64_t n, int64_t k) {

@@ -68,6 +68,8 @@ __device__ __forceinline__ half8 dequant_t2_natural(uint32_t w, int h, uint32_t 
 // (each with its own pair of X buffers), and their accumulators are summed through LDS at the end. A SIMD then holds
 // two waves, so one wave's dequantisation issues while the other's MFMAs run: with one wave per SIMD in-order issue
 // leaves most of the VALU work outside the MFMA shadow. The caller gives W8 an even number of super-steps.
+// NB = 2 (narrow tiles, four waves, dense only): each wave takes 32 columns, a workgroup 128, so shapes with few
+// 256-column tiles need fewer K splits (and fp32 partials) to fill the chip.
 template <int FMT, int MB, int NB, bool ADD, bool SPLIT, int MODE, bool W8>
 __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   const uint32_t* __restrict__ wq = ga.w;
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   constexpr int BM = 16 * MB;
   constexpr int NW = 16 * NB;
   constexpr int FR = MB * 4 * 64;  // uint4 slots per buffer: MB row blocks x 4 steps x 64 lanes
-  static_assert(NB == 4, "the W prefetch issues one column block per MFMA step");
+  static_assert(NB == 4 || (NB == 2 && !W8 && MODE == kDense), "W prefetch: one column block per MFMA step");
   __shared__ uint4 xbuf[(W8 ? 4 : 2) * FR];
 
   int sp = 0, nt, m0, expert = 0;
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
     for (int mb = 0; mb < MB; ++mb) a[0][mb] = __builtin_bit_cast(half8, cur[mb * 256 + aslot + asw]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      load_b(kf, fw.w, fw.s, s);  // NB == 4: one column block per MFMA step
+      if (s < NB) load_b(kf, fw.w, fw.s, s);  // one column block per MFMA step
       if (s < 3) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -240,9 +242,9 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
       __builtin_amdgcn_sched_barrier(0);
     }
     // Vector memory loads complete in issue order: with only this step's 2 * NB W and scale loads still allowed in
-    // flight, this wave's X loads into `nxt` (issued before them) have landed. vmcnt(8), expcnt/lgkmcnt unchanged.
-    static_assert(2 * NB == 8, "the wait below allows exactly the 2 * NB W and scale loads of fw in flight");
-    __builtin_amdgcn_s_waitcnt(0x0F78);
+    // flight, this wave's X loads into `nxt` (issued before them) have landed. vmcnt(2 * NB), expcnt/lgkmcnt
+    // unchanged (T2W issues 3 * NB, so it waits for some of them as well).
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NB));
     __syncthreads();  // ... and everyone's; `cur` may be overwritten from here on
   };
   for (int ks = ks0; ks < ks1; ks += 6) {
@@ -272,11 +274,12 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
 }
 
-template <int FMT, int MB, int MODE, bool W8>
+template <int FMT, int MB, int NB, int MODE, bool W8>
 static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
-  constexpr int NB = 4;
   const dim3 block(W8 ? 512 : 256);
-  if constexpr (MODE == kDense) {
+  if constexpr (NB == 2 && (W8 || MODE != kDense)) {
+    return;  // not built: launch_gemm_x16 refuses these
+  } else if constexpr (MODE == kDense) {
     if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE, W8>), dim3(blocks), block, 0, s, ga);
     else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
     else hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
@@ -285,25 +288,25 @@ static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipS
   }
 }
 
-template <int FMT, int MODE, bool W8>
+template <int FMT, int NB, int MODE, bool W8>
 static void launch_mode(const GemmArgs& ga, int mb, bool add, bool split, int blocks, hipStream_t s) {
   switch (mb) {
-    case 1: return launch_mb<FMT, 1, MODE, W8>(ga, add, split, blocks, s);
-    case 2: return launch_mb<FMT, 2, MODE, W8>(ga, add, split, blocks, s);
-    case 3: return launch_mb<FMT, 3, MODE, W8>(ga, add, split, blocks, s);
-    case 4: return launch_mb<FMT, 4, MODE, W8>(ga, add, split, blocks, s);
-    case 5: return launch_mb<FMT, 5, MODE, W8>(ga, add, split, blocks, s);
-    case 6: return launch_mb<FMT, 6, MODE, W8>(ga, add, split, blocks, s);
-    default: return launch_mb<FMT, 7, MODE, W8>(ga, add, split, blocks, s);
+    case 1: return launch_mb<FMT, 1, NB, MODE, W8>(ga, add, split, blocks, s);
+    case 2: return launch_mb<FMT, 2, NB, MODE, W8>(ga, add, split, blocks, s);
+    case 3: return launch_mb<FMT, 3, NB, MODE, W8>(ga, add, split, blocks, s);
+    case 4: return launch_mb<FMT, 4, NB, MODE, W8>(ga, add, split, blocks, s);
+    case 5: return launch_mb<FMT, 5, NB, MODE, W8>(ga, add, split, blocks, s);
+    case 6: return launch_mb<FMT, 6, NB, MODE, W8>(ga, add, split, blocks, s);
+    default: return launch_mb<FMT, 7, NB, MODE, W8>(ga, add, split, blocks, s);
   }
 }
 
 template <bool W8>
 static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
-  if (fmt == kT2) launch_mode<kT2, kDense, W8>(ga, mb, add, split, blocks, s);
-  else if (mode == kDense) launch_mode<kQ4, kDense, W8>(ga, mb, add, split, blocks, s);
-  else if (mode == kGrouped) launch_mode<kQ4, kGrouped, W8>(ga, mb, false, false, blocks, s);
-  else launch_mode<kQ4, kGroupedSwiglu, W8>(ga, mb, false, false, blocks, s);
+  if (fmt == kT2) launch_mode<kT2, 4, kDense, W8>(ga, mb, add, split, blocks, s);
+  else if (mode == kDense) launch_mode<kQ4, 4, kDense, W8>(ga, mb, add, split, blocks, s);
+  else if (mode == kGrouped) launch_mode<kQ4, 4, kGrouped, W8>(ga, mb, false, false, blocks, s);
+  else launch_mode<kQ4, 4, kGroupedSwiglu, W8>(ga, mb, false, false, blocks, s);
 }
 
 // Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok. Every
@@ -311,9 +314,16 @@ static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split
 // The 8-wave form runs for dense ranges of >= 16 super-steps (same-process A/B: C1's int4 gate|up 40.1 -> 37.8 us,
 // C2's ternary GEMM 5-12% faster; with 2-8 super-steps a group, C1's split-K projections lose 5-10%, and C3's
 // grouped gate|up goes from 84 to 94 us, so those keep four waves).
-int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, bool add, bool split, int mode, int blocks, hipStream_t s) {
+int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, int nb, bool add, bool split, int mode, int blocks,
+                    hipStream_t s) {
   const int nsup = (ga.K + kSuper - 1) / kSuper;
   const int per = ga.sup_per_split;
+  if (nb == 2) {  // narrow tiles: dense, four waves
+    if (mode != kDense) return AQ_ERR_SHAPE;
+    if (fmt == kT2) launch_mode<kT2, 2, kDense, false>(ga, mb, add, split, blocks, s);
+    else launch_mode<kQ4, 2, kDense, false>(ga, mb, add, split, blocks, s);
+    return launch_status();
+  }
   if (mode == kDense && per >= 16 && per % 2 == 0 && nsup % per == 0)
     launch_fmt<true>(ga, fmt, mb, add, split, mode, blocks, s);
   else launch_fmt<false>(ga, fmt, mb, add, split, mode, blocks, s);
