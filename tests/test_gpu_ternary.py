@@ -127,7 +127,8 @@ def _gemm_t2(x, w, s, dev, add_to=None):
 
 @pytest.mark.parametrize("m,n,k,xf32", [(16, 64, 128, False), (412, 256, 1024, False), (100, 300, 256, True),
                                         (412, 12288, 4096, False), (412, 4096, 12288, False), (1, 16, 128, False),
-                                        (33, 100, 640, True), (113, 130, 128, False), (150, 200, 384, False)])
+                                        (33, 100, 640, True), (113, 130, 128, False), (150, 200, 384, False),
+                                        (412, 1024, 4096, False)])
 def test_gemm_t2_kat_bit_exact(dev, m, n, k, xf32):
     """Integer-valued X and power-of-two scales: exact in fp16 MFMA with fp32 accumulation."""
     rng = np.random.default_rng(m + n + k)
