@@ -325,17 +325,23 @@ static GemmPlan plan_tiles(int M, int N, int K, int max_mb, int cols, int fill) 
 
 // 256-column tiles of up to 112 rows, K split to cover the 256 CUs (up to 320 workgroups). For the direct-to-LDS
 // kernel (narrow_ok), shapes whose splits would hold only a few super-steps take 128-column tiles instead, which
-// need fewer splits (and fp32 partials): with <= 4 super-steps a split, tiles of 3 or 4 row blocks, whichever gives
-// more workgroups within one per CU; with <= 8, tiles of up to 7 blocks. Same-process A/B on MI355X at M = 431:
-// q|k|v (3072 x 2048) 23.4 -> 15.9 us (3 blocks, no split), o (2048 x 2048) 22.0 -> 16.2 (4 blocks, 2 splits),
-// down (2048 x 8192) 30.3 -> 28.3 (7 blocks, 4 splits). Longer splits lose: the ternary 4096 x 12288 at M = 412
-// went from 48 to 54 us with 7 blocks and 64 with 4.
+// need fewer splits (and fp32 partials): with <= 4 super-steps a split, tiles of 2, 3 or 4 row blocks, whichever
+// gives the most workgroups within one per CU (fewer splits on a tie); with <= 8, tiles of up to 7 blocks.
+// Same-process A/B on MI355X at M = 431: q|k|v (3072 x 2048) 23.4 -> 15.9 us (3 blocks, no split), o (2048 x 2048)
+// 22.0 -> 12.8 (2 blocks, no split; 4 blocks and 2 splits: 16.2), down (2048 x 8192) 30.3 -> 28.3 (7 blocks,
+// 4 splits). Longer splits lose: the ternary 4096 x 12288 at M = 412 went from 48 to 54 us with 7 blocks and 64
+// with 4.
 static GemmPlan plan_gemm(int M, int N, int K, bool narrow_ok) {
   const GemmPlan p = plan_tiles(M, N, K, kMaxMB, 256, 320);
   if (!narrow_ok || p.splits == 1 || p.sup_per_split > 8) return p;
   if (p.sup_per_split > 4) return plan_tiles(M, N, K, kMaxMB, 128, 256);
-  const GemmPlan a = plan_tiles(M, N, K, 3, 128, 256), b = plan_tiles(M, N, K, 4, 128, 256);
-  return a.mtiles * a.ntiles * a.splits > b.mtiles * b.ntiles * b.splits ? a : b;
+  GemmPlan best = plan_tiles(M, N, K, 4, 128, 256);
+  for (int mb = 2; mb < 4; ++mb) {  // more workgroups within one per CU; fewer splits on a tie
+    const GemmPlan c = plan_tiles(M, N, K, mb, 128, 256);
+    const int wc = c.mtiles * c.ntiles * c.splits, wb = best.mtiles * best.ntiles * best.splits;
+    if (wc <= 256 && (wc > wb || (wc == wb && c.splits < best.splits))) best = c;
+  }
+  return best;
 }
 
 static int64_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
