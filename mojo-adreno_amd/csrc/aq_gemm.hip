@@ -433,20 +433,23 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
 }
 
 // ---- grouped (MoE) GEMM ----------------------------------------------------------------------------------------
+// Grouped tiles are 128 columns wide (64 of gate and 64 of up in the SwiGLU form): twice the workgroups of 256-column
+// tiles, which hides more of the weight stream's latency. C3 (T = 404, 48-row tiles): 0.183 -> 0.153 ms a block.
+constexpr int kGroupedNB = 2;
 template <int MB, bool G32, bool XF32, int MODE>
 static int launch_grouped(const GemmArgs& ga0, int max_tiles, hipStream_t s) {
   constexpr int NB = 4;
   const size_t lds = 2 * (size_t)MB * 256 * 16;
   auto kern = k_gemm<kQ4, MB, NB, G32, XF32, false, false, MODE>;
   GemmArgs ga = ga0;
-  ga.ntiles = MODE == kGroupedSwiglu ? (ga.F + 2 * 16 * NB - 1) / (2 * 16 * NB) : (ga.N + 64 * NB - 1) / (64 * NB);
+  const bool x16 = G32 && !XF32 && x16_shape_ok(ga.K, ga.group);
+  const int nbx = x16 ? kGroupedNB : NB;
+  ga.ntiles = MODE == kGroupedSwiglu ? (ga.F + 2 * 16 * nbx - 1) / (2 * 16 * nbx) : (ga.N + 64 * nbx - 1) / (64 * nbx);
   ga.splits = 1;
   ga.sup_per_split = (ga.K + kSuper - 1) / kSuper;
   const int blocks = ga.ntiles * max_tiles;
   if (blocks <= 0) return AQ_OK;
-  if constexpr (G32 && !XF32) {
-    if (x16_shape_ok(ga.K, ga.group)) return launch_gemm_x16(ga, kQ4, MB, 4, false, false, MODE, blocks, s);
-  }
+  if (x16) return launch_gemm_x16(ga, kQ4, MB, nbx, false, false, MODE, blocks, s);
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ga);
   return launch_status();
 }

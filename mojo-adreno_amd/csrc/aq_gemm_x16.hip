@@ -78,7 +78,7 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   constexpr int BM = 16 * MB;
   constexpr int NW = 16 * NB;
   constexpr int FR = MB * 4 * 64;  // uint4 slots per buffer: MB row blocks x 4 steps x 64 lanes
-  static_assert(NB == 4 || (NB == 2 && MODE == kDense), "W prefetch: one column block per MFMA step");
+  static_assert(NB == 4 || (NB == 2 && (MODE == kDense || !W8)), "W prefetch: one column block per MFMA step");
   __shared__ uint4 xbuf[(W8 ? 4 : 2) * FR];
 
   int sp = 0, nt, m0, expert = 0;
@@ -277,8 +277,8 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
 template <int FMT, int MB, int NB, int MODE, bool W8>
 static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
   const dim3 block(W8 ? 512 : 256);
-  if constexpr (NB == 2 && MODE != kDense) {
-    return;  // not built: launch_gemm_x16 refuses these
+  if constexpr (NB == 2 && MODE != kDense && W8) {
+    return;  // not built: grouped launches keep four waves
   } else if constexpr (MODE == kDense) {
     if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE, W8>), dim3(blocks), block, 0, s, ga);
     else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
@@ -309,7 +309,7 @@ static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split
   else launch_mode<kQ4, 4, kGroupedSwiglu, W8>(ga, mb, false, false, blocks, s);
 }
 
-// Grouped modes take neither `add` nor split-K, and Q4W only; narrow tiles (nb = 2) are dense only. The caller has checked x16_shape_ok. Every
+// Grouped modes take neither `add` nor split-K, and Q4W only. The caller has checked x16_shape_ok. Every
 // workgroup's super-step range has the same even length when sup_per_split is even and divides the super-step count.
 // The 8-wave form runs for dense ranges of >= 16 super-steps (same-process A/B: C1's int4 gate|up 40.1 -> 37.8 us,
 // C2's ternary GEMM 5-12% faster; with 2-8 super-steps a group, C1's split-K projections lose 5-10%, and C3's
@@ -320,9 +320,10 @@ int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, int nb, bool add, bool 
   const int nsup = (ga.K + kSuper - 1) / kSuper;
   const int per = ga.sup_per_split;
   const bool w8 = per >= 16 && per % 2 == 0 && nsup % per == 0;
-  if (nb == 2) {  // narrow tiles: dense only
-    if (mode != kDense) return AQ_ERR_SHAPE;
-    if (w8) {
+  if (nb == 2) {  // narrow tiles
+    if (mode == kGrouped) launch_mode<kQ4, 2, kGrouped, false>(ga, mb, false, false, blocks, s);
+    else if (mode == kGroupedSwiglu) launch_mode<kQ4, 2, kGroupedSwiglu, false>(ga, mb, false, false, blocks, s);
+    else if (w8) {
       if (fmt == kT2) launch_mode<kT2, 2, kDense, true>(ga, mb, add, split, blocks, s);
       else launch_mode<kQ4, 2, kDense, true>(ga, mb, add, split, blocks, s);
     } else {

@@ -170,7 +170,7 @@ def test_grouped_gemm_kat_exact(dev):
         np.testing.assert_array_equal(got[row], exact[0].astype(np.float32))
 
 
-@pytest.mark.parametrize("t,tm", [(404, 32), (404, 48), (64, 16)])
+@pytest.mark.parametrize("t,tm", [(404, 32), (404, 48), (404, 64), (64, 16)])
 def test_c3_moe_block(dev, t, tm):
     """C3: Qwen3-30B-A3B-shaped block (128 experts, D 2048, F 768, G 32, top 8), fp32 x, vs the oracle."""
     import torch
