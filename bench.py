@@ -445,6 +445,32 @@ def cpu_baseline_gemv():
                        f"{cb.cpu_model()}; dequant+mv {per / t_all / 1e9:.2f} GB/s")
 
 
+def cpu_baseline_ternary():
+    from aq import synth
+    from oracle import cpu_baseline as cb
+    cores = cb.threads()
+    d = synth.c2()
+    t_mv, t_mm = cb.ternary(d["mats"], d["xv"], d["x"])
+    per = sum(_t2_gemv_bytes(n, k) for _, n, k in C2_MATS)
+    flop = sum(2 * d["tokens"] * n * k for _, n, k in C2_MATS)
+    return dict(value=round(per / t_mv / 1e9, 2), unit="GB/s", cores=cores, kind="port",
+                gemm_tflops=round(flop / t_mm / 1e12, 4),
+                sample=f"C2 gate, up and down (12288x4096, 12288x4096, 4096x12288): torch fp32 mv (value, over the "
+                       f"triple's T2W bytes) and F.linear at M={d['tokens']} (gemm_tflops) over the dequantised "
+                       f"matrices, median of <=20 / <=5 reps on {cb.cpu_model()}")
+
+
+def cpu_baseline_moe():
+    from aq import synth
+    from oracle import cpu_baseline as cb
+    cores = cb.threads()
+    t = cb.moe_block(synth.c3())
+    return dict(value=round(t * 1e3, 3), unit="ms", cores=cores, kind="port",
+                sample=f"C3 block at 404 tokens: transformers-style fp32 torch (softmax, top-8, renormalise, loop over "
+                       f"the hit experts with index_add_) over dequantised experts, median of <=5 reps on "
+                       f"{cb.cpu_model()}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -507,6 +533,8 @@ def main():
         out["cpu_baseline"] = cpu_baseline_gemm()
         out["gemv_c0"]["cpu_baseline"] = cpu_baseline_gemv()
         out["decode_c4"]["cpu_baseline"] = cpu_baseline_decode()
+        out["ternary_c2"]["cpu_baseline"] = cpu_baseline_ternary()
+        out["moe_c3"]["cpu_baseline"] = cpu_baseline_moe()
     print(json.dumps(out), flush=True)
 
 

@@ -1,8 +1,9 @@
 """CPU baseline for bench.py: the reference's own CPU path, restated. TEST/MEASUREMENT INFRASTRUCTURE ONLY.
 
 The reference checks this arithmetic on the CPU with PyTorch over *dequantised* weights: qwen3moe/reference.py:53-65
-dequantises the int4 words with numpy and runs fp32 torch layers (:121-129); llama/run.py:77-86,186-198 does the
-same for Llama. This module restates that path with torch on the host cores (fp32 ``F.linear`` over a dequantised
+dequantises the int4 words with numpy and runs fp32 torch layers (:121-129), its MoE block as transformers'
+Qwen3MoeSparseMoeBlock (softmax, top-k, renormalise, a loop over the hit experts with ``index_add_``); llama/run.py:
+77-86,186-198 does the same for Llama. This module restates that path with torch on the host cores (fp32 ``F.linear`` over a dequantised
 matrix; dequantisation timed separately), so bench.py can report it beside the GPU numbers. Only bench.py's
 ``cpu_baseline`` leg imports it.
 """
@@ -121,3 +122,58 @@ def llama_decode(mats: dict, head: tuple, dim: int, heads: int, kv_heads: int, f
         return int(torch.argmax(F.linear(rms(x0), lm)))
 
     return median_time(layers, reps, budget_s / 2), median_time(head_fn, reps, budget_s / 2)
+
+
+def dequant_t2(w: np.ndarray, s: np.ndarray) -> torch.Tensor:
+    """T2W words [K/16, N] and fp16 scales [K/128, N] -> fp32 [N, K]: ``(code - 1) * scale`` with code (k, n) at bits
+    2 (k % 16) of word (k / 16, n) (bonsai/kernels/prefill.mojo:228-230,260)."""
+    wt = torch.from_numpy(np.ascontiguousarray(w).view(np.int32))
+    shifts = torch.arange(0, 32, 2, dtype=torch.int32)
+    codes = (wt.unsqueeze(-1) >> shifts) & 3                       # [K/16, N, 16]
+    q = (codes.permute(1, 0, 2).reshape(wt.shape[1], -1) - 1).to(torch.float32)
+    sc = torch.from_numpy(np.ascontiguousarray(s).astype(np.float32)).t()  # [N, K/128]
+    return (q.reshape(q.shape[0], -1, 128) * sc.unsqueeze(-1)).reshape(q.shape)
+
+
+def ternary(mats: dict, xv: dict, xs: dict, reps=5, budget_s=8.0):
+    """Seconds for one gate/up/down triple of fp32 ``mv`` (the GEMV) and of ``F.linear`` at M rows (the GEMM) over
+    the dequantised ternary matrices. ``mats[name] = (words, scales)``; xv / xs keyed by K."""
+    ws = [dequant_t2(w, s) for w, s in mats.values()]
+    v = {k: torch.from_numpy(np.asarray(a, np.float32)) for k, a in xv.items()}
+    m = {k: torch.from_numpy(np.asarray(a, np.float32)) for k, a in xs.items()}
+    t_mv = median_time(lambda: [torch.mv(w, v[w.shape[1]]) for w in ws], reps * 4, budget_s / 2)
+    t_mm = median_time(lambda: [torch.nn.functional.linear(m[w.shape[1]], w) for w in ws], reps, budget_s / 2)
+    return t_mv, t_mm
+
+
+def moe_block(d: dict, reps=5, budget_s=10.0):
+    """Seconds for one MoE block over d["tokens"] tokens (``moe_forward``)."""
+    return median_time(moe_forward(d), reps, budget_s)
+
+
+def moe_forward(d: dict, topk: int = 8):
+    """One MoE block over d["tokens"] tokens as transformers' Qwen3MoeSparseMoeBlock computes it in fp32 on
+    dequantised experts (qwen3moe/reference.py:121-129): softmax of the router logits, top-k, renormalise, then for
+    every expert that was hit, ``down(silu(gate x) * up x)`` of its tokens times their weights, ``index_add_`` into
+    the output. Returns the block as a function of no arguments (the experts dequantised once)."""
+    E, D, F, G = d["experts"], d["hidden"], d["ffn"], d["group"]
+    gu = dequant_q4(d["gu_q"], d["gu_s"], G).view(E, 2 * F, D)
+    dn = dequant_q4(d["dn_q"], d["dn_s"], G).view(E, D, F)
+    x = torch.from_numpy(d["x"])
+    logits = torch.from_numpy(d["logits"])
+    lin = torch.nn.functional.linear
+
+    def run():
+        p = torch.softmax(logits, dim=-1)
+        w, ids = torch.topk(p, topk, dim=-1)
+        w = w / w.sum(dim=-1, keepdim=True)
+        out = torch.zeros_like(x)
+        mask = torch.nn.functional.one_hot(ids, E).permute(2, 1, 0)  # [E, topk, T]
+        for e in torch.nonzero(mask.sum(dim=(1, 2))).flatten().tolist():
+            slot, tok = torch.where(mask[e])
+            h = lin(x[tok], gu[e])
+            y = lin(torch.nn.functional.silu(h[:, :F]) * h[:, F:], dn[e]) * w[tok, slot, None]
+            out.index_add_(0, tok, y)
+        return out
+
+    return run

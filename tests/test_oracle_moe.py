@@ -118,3 +118,18 @@ def test_moe_layer_per_token_brute_force():
             a = h[:f] / (1 + np.exp(-h[:f])) * h[f:]
             acc += w[tt, kk] * (dn[ex * d:(ex + 1) * d] @ a)
         np.testing.assert_allclose(y[tt], acc, rtol=1e-10, atol=1e-12)
+
+
+def test_cpu_baseline_restatements_match_the_oracle():
+    """bench.py's CPU baseline computes what the oracle computes: its transformers-style MoE block (softmax, top-k,
+    renormalise, per-expert loop with index_add_) and its ternary dequantisation (the float64 oracle, to fp32
+    rounding), so the time it reports is for the same work."""
+    from aq import synth
+    from oracle import cpu_baseline as cb
+    d = synth.c3(tokens=24, experts=8, hidden=64, ffn=32)
+    got = cb.moe_forward(d, topk=2)().numpy()
+    ref, _, _ = orc.moe_layer(d["x"], d["logits"], d["gu_q"], d["gu_s"], d["dn_q"], d["dn_s"], 32, 32, topk=2)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5 * np.abs(ref).max())
+    rng = np.random.default_rng(5)
+    w, s = synth.ternary_matrix(rng, 48, 256)
+    np.testing.assert_array_equal(cb.dequant_t2(w, s).numpy(), orc.t2w_dequant(w, s).astype(np.float32))
