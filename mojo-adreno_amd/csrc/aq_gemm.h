@@ -59,6 +59,11 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& ga, int BM, int& sp, int
 
 // Epilogue shared by the GEMM kernels: lane l holds D[4*(l/16) + r][l%16] of each 16x16 tile; buffer stores drop rows
 // and columns past the end.
+// Cache policy of the dense GEMM's final fp32 output stores: sc1 | nt (streaming, device scope); the output is
+// written once at the end of a one-pass launch. bench.py on MI355X, alternating libraries: C1 gate|up 42.3 -> 41.5 us,
+// C2's ternary GEMM 159 -> 154 us a triple. Split-K partials (read back by k_splitk_reduce) and the grouped outputs
+// (read back by the combine: the C3 block was 3% slower with nt) keep the default policy.
+constexpr int kYPolicy = 18;
 template <int MB, int NB, bool ADD, bool SPLIT, int MODE>
 __device__ __forceinline__ void gemm_store(const GemmArgs& ga, const float4v (&acc)[MB][NB], int m0, int nw0, int sp,
                                            int lane) {
@@ -100,7 +105,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& ga, const float4v (&a
           float v = acc[mb][nb][r];
           if constexpr (ADD && !SPLIT)
             v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0,
+                                                (MODE == kDense && !SPLIT) ? kYPolicy : 0);
         }
       }
     }
