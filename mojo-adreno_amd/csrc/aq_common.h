@@ -89,6 +89,17 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return __builtin_bit_cast(uint4, v);
 }
+// The same with a cache policy (for data read once, such as the weights of a decode GEMV).
+// kWPolicy: nt (streaming). The matrix-vector kernels read each weight once a launch; bench.py on MI355X, alternating
+// libraries: the C4 decode step 486 -> 463 us, C0 4.83 -> 4.73 us, the int4 lm_head 38.3 -> 37.3 us, C2's ternary
+// GEMV triple 21.8 -> 21.2 us, the ternary head 35.8 -> 34.1 us (sc1 | nt and sc0 | nt measured the same). Not for
+// loads whose pieces share cache lines (the Q6_K head).
+constexpr int kWPolicy = 2;
+template <int POL>
+__device__ __forceinline__ uint4 buf_load16p(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
+  return __builtin_bit_cast(uint4, v);
+}
 
 __device__ __forceinline__ float buf_load_half(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);

@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       const uint32_t row = gemv_row<MODE, RO>(ib, r, n_out, f, moe);  // a valid row even past the end
       const uint32_t wo = (row * (uint32_t)kw + 4 * c) * 4;
       const uint32_t si = row * (uint32_t)gpr + ((32 * c) >> gsh);
-      w[r] = buf_load16(w_rsrc, ok ? wo : kOOB);
+      w[r] = buf_load16p<kWPolicy>(w_rsrc, ok ? wo : kOOB);
       sc[r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, ok ? (si * 2) & ~3u : kOOB, 0, 0);
       sb[r] = (si & 1) << 4;
     }

@@ -33,6 +33,8 @@ struct Q6Raw {
 __device__ __forceinline__ void q6_load(__amdgpu_buffer_rsrc_t qr, __amdgpu_buffer_rsrc_t dr, uint32_t blk,
                                         uint32_t dof, int h, int g, Q6Raw& r) {
   const uint32_t ql = blk + 64 * h + 32 * g, qh = blk + 128 + 32 * h;
+  // default cache policy: the four 16-byte pieces of a unit share cache lines (streaming loads measured 50.8 -> 79 us
+  // on the LFM2 head)
   r.l0 = buf_load16(qr, ql);
   r.l1 = buf_load16(qr, ql + 16);
   r.h0 = buf_load16(qr, qh);

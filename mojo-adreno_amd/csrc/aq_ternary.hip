@@ -158,13 +158,13 @@ __global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict_
       const uint32_t row = (uint32_t)(kr0 + r0 + r);
       if constexpr (VEC4) {
         const uint32_t off = n0 < N ? (row * (uint32_t)N + n0) * 4 : 0x80000000u;
-        wv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+        wv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, kWPolicy));
       } else {
         uint32_t v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const uint32_t off = n0 + c < N ? (row * (uint32_t)N + n0 + c) * 4 : 0x80000000u;
-          v[c] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
+          v[c] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, kWPolicy);
         }
         wv[r] = make_uint4(v[0], v[1], v[2], v[3]);
       }
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
 #pragma unroll
     for (int r = 0; r < 8; ++r)
       wv[r] = __builtin_amdgcn_raw_buffer_load_b32(wr, col_ok ? ((uint32_t)(g * 8 + r) * N + n) * 4 : 0x80000000u, 0,
-                                                   0);
+                                                   kWPolicy);
     const float s = half_bits_to_float(
         __builtin_amdgcn_raw_buffer_load_b16(srs, col_ok ? ((uint32_t)g * N + n) * 2 : 0x80000000u, 0, 0));
     float acc0 = -gbias[g], acc1 = 0.f;  // two chains: even and odd rows
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void k_t2_gemv_wide(const uint32_t* __restrict
   auto issue = [&](int g, uint4 (&wv)[8], uint32_t (&s)[2]) {
     const bool v = ok && g < groups;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) wv[r] = buf_load16(wr, v ? ((uint32_t)(g * 8 + r) * N + n0) * 4 : kOOB);
+    for (int r = 0; r < 8; ++r) wv[r] = buf_load16p<kWPolicy>(wr, v ? ((uint32_t)(g * 8 + r) * N + n0) * 4 : kOOB);
     const uint2 t = __builtin_bit_cast(
         uint2, __builtin_amdgcn_raw_buffer_load_b64(sr, v ? ((uint32_t)g * N + n0) * 2 : kOOB, 0, 0));
     s[0] = t.x, s[1] = t.y;
