@@ -31,6 +31,8 @@ def _gemm(x, wq, ws, group, dev, add_to=None):
     (113, 130, 128, 32, False), (150, 200, 512, 32, False), (240, 1000, 384, 64, False), (700, 384, 256, 32, False),
     # narrow 128-column tiles in the eight-wave form (>= 16 super-steps a workgroup): the fused q|k|v of C1
     (431, 3072, 2048, 32, False),
+    # one pass that would leave CUs idle takes shorter tiles (2 x 81 tiles of 7 blocks -> 3 x 81 of 5)
+    (200, 20736, 128, 32, False),
 ])
 def test_kat_bit_exact(dev, m, n, k, group, xf32):
     """Integer-valued X, power-of-two scales: exact in fp16 and in fp32 accumulation, so the MFMA result must equal
