@@ -178,7 +178,8 @@ def _t2_head_argmax_impl(x2h, w, s, logits, cand, token, pos, hist, advance):
     _dev(logits, cand, token, pos, hist)
     _check(logits.dtype == torch.float32 and logits.numel() == n, "logits must be float32 [N]")
     _check(cand.dtype == torch.int64, "cand must be int64")
-    _check(token.dtype == torch.int32 and pos.dtype == torch.int32 and hist.dtype == torch.int32, "int32 token/pos/hist")
+    _check(token.dtype == torch.int32 and pos.dtype == torch.int32 and hist.dtype == torch.int32,
+           "int32 token/pos/hist")
     _lib.call("aq_t2_head_argmax", _ptr(x2h), _ptr(w), _ptr(s), _ptr(logits), n, k, _ptr(cand), cand.numel(),
               _ptr(token), _ptr(pos), _ptr(hist) if hist.numel() else None, hist.numel(), advance, _stream(logits))
 
@@ -295,7 +296,8 @@ def gemm_t2(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, y: torch.Tensor, 
 # ---- mixture of experts -------------------------------------------------------------------------------------------
 
 _LIB.define("moe_route(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk) -> ()")
-_LIB.define("moe_route_pack(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk, Tensor x, Tensor(c!) xq) -> ()")
+_LIB.define("moe_route_pack(Tensor logits, Tensor(a!) ids, Tensor(b!) weights, int topk, Tensor x, "
+            "Tensor(c!) xq) -> ()")
 _LIB.define("moe_group(Tensor ids, int experts, int tm, Tensor(a!) counts, Tensor(b!) offs, Tensor(c!) slot, "
             "Tensor(d!) src, Tensor(e!) tiles, Tensor(f!) ntiles) -> ()")
 _LIB.define("moe_gemm_q4(Tensor x, Tensor src, Tensor wq, Tensor ws, int experts, int group, Tensor tiles, "
@@ -422,8 +424,8 @@ def _moe_expert_lists_impl(ids, experts, lists, counts, items_tt, items, nitems,
               items_ptr, items.numel() // 2, nitems_ptr, _ptr(scratch), scratch.numel(), _stream(ids))
 
 
-for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route_pack_impl), ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl),
-                   ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
+for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route_pack_impl),
+                   ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl), ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
                    ("moe_down_q4", _moe_down_q4_impl), ("gemv_f32", _gemv_f32_impl),
                    ("moe_expert_lists", _moe_expert_lists_impl)):
     _LIB.impl(_name, _fn, "CUDA")
@@ -467,7 +469,8 @@ def _rmsnorm_gemv_q4_impl(wq, ws, x, norm_w, eps, y, group):
     _f16bits(norm_w, "norm_w")
     _check(x.dtype == torch.float32 and y.dtype == torch.float32, "x and y must be float32")
     tokens = x.numel() // k
-    _check(x.numel() == tokens * k and y.numel() == tokens * n and norm_w.numel() == k, "x [T, K], y [T, N], norm_w [K]")
+    _check(x.numel() == tokens * k and y.numel() == tokens * n and norm_w.numel() == k,
+           "x [T, K], y [T, N], norm_w [K]")
     _lib.call("aq_rmsnorm_gemv_q4", _ptr(wq), _ptr(ws), _ptr(x), _ptr(norm_w), eps, _ptr(y), n, k, group, tokens,
               _stream(x))
 
