@@ -3,8 +3,8 @@
 
 Prompt (T tokens): route (top-k of the router logits) -> group (device histogram, padded prefix sum, stable
 permute, work tiles of ``tm`` rows) -> fp32 tokens rounded to fp16 once -> grouped gate|up GEMM with the SwiGLU
-product in its epilogue (fp16 activations) -> grouped down GEMM -> weighted combine in k order (+ residual). Decode (one token): route -> gate|up
-over the k chosen experts -> down summed over them. All buffers are allocated once, at construction, for at most
+product in its epilogue (fp16 activations) -> grouped down GEMM -> weighted combine in k order (+ residual). Decode
+(one token): route -> gate|up over the k chosen experts -> down summed over them. All buffers are allocated once, at construction, for at most
 ``max_tokens`` tokens; a forward call allocates nothing and never synchronises with the host.
 """
 from __future__ import annotations

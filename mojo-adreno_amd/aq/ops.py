@@ -425,7 +425,8 @@ def _moe_expert_lists_impl(ids, experts, lists, counts, items_tt, items, nitems,
 
 
 for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route_pack_impl),
-                   ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl), ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
+                   ("moe_group", _moe_group_impl), ("moe_gemm_q4", _moe_gemm_q4_impl),
+                   ("moe_combine", _moe_combine_impl), ("moe_gate_up_q4", _moe_gate_up_q4_impl),
                    ("moe_down_q4", _moe_down_q4_impl), ("gemv_f32", _gemv_f32_impl),
                    ("moe_expert_lists", _moe_expert_lists_impl)):
     _LIB.impl(_name, _fn, "CUDA")
