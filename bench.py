@@ -242,26 +242,37 @@ def _t2_gemv_bytes(n, k):
     return (k // 16) * n * 4 + (k // 128) * n * 2 + k * 2 + n * 4
 
 
-C2_MATS = (("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288))
+# The reference's Qwen3 MLP: gate and up fused along N into one T2W matrix "gu" (qwen3/convert.cpp:118), one
+# projection over 2F outputs (qwen3/model.mojo:165 decode, :230 prefill), then down.
+C2_MATS = (("gu", 24576, 4096), ("down", 4096, 12288))
+
+
+def _c2_first(rng):
+    """Copy 0 of the C2 weights from the seeded generator: gate and up (12288 x 4096) fused along N, then down."""
+    import numpy as np
+    from aq import synth
+    g, u, d = (synth.ternary_matrix(rng, n, k) for n, k in ((12288, 4096), (12288, 4096), (4096, 12288)))
+    return {"gu": (np.concatenate([g[0], u[0]], axis=1), np.concatenate([g[1], u[1]], axis=1)), "down": d}
 
 
 def bench_ternary_c2(dev, pool_mb: int = 560):
-    """C2: ternary GEMV (M=1) over a rotating pool of distinct gate/up/down triples, and ternary GEMM at M=412."""
+    """C2: ternary GEMV (M=1) over a rotating pool of distinct MLP weight sets (gate|up fused, down), and ternary GEMM
+    at M=412."""
     import numpy as np
     import torch
     from aq import ops, synth
     gen = torch.Generator(device=dev)
     gen.manual_seed(102)
-    per_triple = sum(_t2_gemv_bytes(n, k) for _, n, k in C2_MATS)
-    copies = max(2, int(pool_mb * 1e6 // per_triple))
+    per_layer = sum(_t2_gemv_bytes(n, k) for _, n, k in C2_MATS)
+    copies = max(2, int(pool_mb * 1e6 // per_layer))
     rng = np.random.default_rng(2)
+    first = _c2_first(rng)
     mats = []
     for c in range(copies):
         trip = {}
         for name, n, k in C2_MATS:
             if c == 0:
-                w, s_ = synth.ternary_matrix(rng, n, k)
-                trip[name] = (_dev(w, dev), _dev(s_, dev))
+                trip[name] = (_dev(first[name][0], dev), _dev(first[name][1], dev))
             else:  # random 2-bit codes (3 would decode to +2; timing does not depend on the values)
                 w = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 16, n), dtype=torch.int32, device=dev, generator=gen)
                 s_ = (torch.rand((k // 128, n), device=dev, generator=gen) * 0.02).to(torch.float16)
@@ -272,8 +283,8 @@ def bench_ternary_c2(dev, pool_mb: int = 560):
     launches = [(lambda w=m[name][0], s_=m[name][1], k=k, y=ys[name]: ops.t2_gemv(xh[k], w, s_, y))
                 for m in mats for name, _, k in C2_MATS]
     t_all = GraphTimer(launches).time(replays=3)
-    gemv = dict(gbs=round(copies * per_triple / t_all / 1e9, 2), us_per_triple=round(t_all / copies * 1e6, 3),
-                frac_hbm=round(copies * per_triple / t_all / 1e9 / HBM_PEAK_GBS, 4), pool_mb=round(copies * per_triple / 1e6, 1))
+    gemv = dict(gbs=round(copies * per_layer / t_all / 1e9, 2), us_per_layer=round(t_all / copies * 1e6, 3),
+                frac_hbm=round(copies * per_layer / t_all / 1e9 / HBM_PEAK_GBS, 4), pool_mb=round(copies * per_layer / 1e6, 1))
     m = synth.C2_GEMM_TOKENS
     xs = {k: torch.randn((m, k), device=dev, generator=gen).to(torch.float16) for k in (4096, 12288)}
     yg = {name: torch.empty((m, n), dtype=torch.float32, device=dev) for name, n, _ in C2_MATS}
@@ -281,7 +292,7 @@ def bench_ternary_c2(dev, pool_mb: int = 560):
           for mm in mats[:4] for name, _, k in C2_MATS]
     t_g = GraphTimer(gl).time(replays=3) / min(4, copies)
     flop = sum(2 * m * n * k for _, n, k in C2_MATS)
-    gemm = dict(tflops=round(flop / t_g / 1e12, 2), us_per_triple=round(t_g * 1e6, 3),
+    gemm = dict(tflops=round(flop / t_g / 1e12, 2), us_per_layer=round(t_g * 1e6, 3),
                 frac_mfma=round(flop / t_g / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), tokens=m)
     return dict(gemv=gemv, gemm=gemm)
 
@@ -449,14 +460,18 @@ def cpu_baseline_ternary():
     from aq import synth
     from oracle import cpu_baseline as cb
     cores = cb.threads()
+    import numpy as np
     d = synth.c2()
-    t_mv, t_mm = cb.ternary(d["mats"], d["xv"], d["x"])
+    g, u = d["mats"]["gate"], d["mats"]["up"]
+    mats = {"gu": (np.concatenate([g[0], u[0]], axis=1), np.concatenate([g[1], u[1]], axis=1)),
+            "down": d["mats"]["down"]}
+    t_mv, t_mm = cb.ternary(mats, d["xv"], d["x"])
     per = sum(_t2_gemv_bytes(n, k) for _, n, k in C2_MATS)
     flop = sum(2 * d["tokens"] * n * k for _, n, k in C2_MATS)
     return dict(value=round(per / t_mv / 1e9, 2), unit="GB/s", cores=cores, kind="port",
                 gemm_tflops=round(flop / t_mm / 1e12, 4),
-                sample=f"C2 gate, up and down (12288x4096, 12288x4096, 4096x12288): torch fp32 mv (value, over the "
-                       f"triple's T2W bytes) and F.linear at M={d['tokens']} (gemm_tflops) over the dequantised "
+                sample=f"C2 MLP, gate|up fused (24576x4096) and down (4096x12288): torch fp32 mv (value, over the "
+                       f"layer's T2W bytes) and F.linear at M={d['tokens']} (gemm_tflops) over the dequantised "
                        f"matrices, median of <=20 / <=5 reps on {cb.cpu_model()}")
 
 

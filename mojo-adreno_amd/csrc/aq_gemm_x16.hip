@@ -315,11 +315,15 @@ static void launch_fmt(const GemmArgs& ga, int fmt, int mb, bool add, bool split
 // C2's ternary GEMM 5-12% faster; with 2-8 super-steps a group, C1's split-K projections lose 5-10%, and C3's
 // grouped gate|up goes from 84 to 94 us, so those keep four waves). Narrow tiles follow the same rule (C1's q|k|v
 // with 16 super-steps a workgroup: 16.1 -> 15.0 us).
+// The eight-wave form takes a whole CU (512 threads, up to 112 KB of LDS); above one workgroup per CU, four waves let
+// two workgroups share a CU instead of running a second, partial round: C2's fused ternary gate|up (24576 x 4096 at
+// M = 412, 384 workgroups) 96.0 -> 84.6 us.
+constexpr int kW8MaxBlocks = 256;
 int launch_gemm_x16(const GemmArgs& ga, int fmt, int mb, int nb, bool add, bool split, int mode, int blocks,
                     hipStream_t s) {
   const int nsup = (ga.K + kSuper - 1) / kSuper;
   const int per = ga.sup_per_split;
-  const bool w8 = per >= 16 && per % 2 == 0 && nsup % per == 0;
+  const bool w8 = per >= 16 && per % 2 == 0 && nsup % per == 0 && blocks <= kW8MaxBlocks;
   if (nb == 2) {  // narrow tiles
     if (mode == kGrouped) launch_mode<kQ4, 2, kGrouped, false>(ga, mb, false, false, blocks, s);
     else if (mode == kGroupedSwiglu) launch_mode<kQ4, 2, kGroupedSwiglu, false>(ga, mb, false, false, blocks, s);

@@ -33,6 +33,8 @@ def _gemm(x, wq, ws, group, dev, add_to=None):
     (431, 3072, 2048, 32, False),
     # one pass that would leave CUs idle takes shorter tiles (2 x 81 tiles of 7 blocks -> 3 x 81 of 5)
     (200, 20736, 128, 32, False),
+    # more than 256 workgroups with 16 super-steps each: the four-wave form, two workgroups a CU
+    (16, 65792, 2048, 32, False),
 ])
 def test_kat_bit_exact(dev, m, n, k, group, xf32):
     """Integer-valued X, power-of-two scales: exact in fp16 and in fp32 accumulation, so the MFMA result must equal
