@@ -89,29 +89,16 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   const int gpr = k / group;
   constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
   constexpr int SL = MODE == kMoeDown ? T : 1;  // weight rows per output (kMoeDown: one per expert slot)
-  // G32 dense products (kStore, kAdd, kGateUp) stream the wave's chunks, over all its row blocks, through D register
-  // sets: D chunks are in flight while one is used (with D > 1 the last D requests fall past the end and carry an
-  // out-of-range offset; with D = 1 nothing is requested past the end). kMoeGateUp (rows from device expert ids)
-  // double-buffers within a row block. The rest (kMoeDown, groups that are not powers of two >= 32) request each chunk
-  // when they use it.
-  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp);
-  constexpr bool kPipe = G32 && MODE == kMoeGateUp;
+  // G32 products but kMoeDown (kStore, kAdd, kGateUp, and kMoeGateUp with rows from device expert ids) stream the
+  // wave's chunks, over all its row blocks, through D register sets: D chunks are in flight while one is used (with
+  // D > 1 the last D requests fall past the end and carry an out-of-range offset; with D = 1 nothing is requested
+  // past the end). The rest (kMoeDown, groups that are not powers of two >= 32) request each chunk when they use it.
+  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp || MODE == kMoeGateUp);
   const int stride = gridDim.x * 4 * RO;
   const int cpl = (nch + kWave - 1) / kWave;  // chunks per lane and row block (the last may be partial)
 
-  // one chunk (16 bytes = 32 weights of each of the R rows, and their G32 scales); only kMoeGateUp can name no row
-  // (an invalid expert id): its weights read as zero codes with scale 0
   // scales travel as raw fp16 bits and are converted where used: a conversion next to its load would wait for it
   const int gsh = __builtin_ctz(group);  // G32 groups are powers of two
-  auto load_chunk = [&](const int (&rows)[R], int c, uint4 (&w)[R], uint16_t (&sc)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const bool ok = MODE != kMoeGateUp || rows[r] >= 0;
-      w[r] = ok ? *reinterpret_cast<const uint4*>(wq + (size_t)rows[r] * kw + c * 4)
-                : make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-      sc[r] = ok ? ws[(size_t)rows[r] * gpr + ((c * 32) >> gsh)] : (uint16_t)0;
-    }
-  };
   // One chunk: each word's 8 codes become 4 fp16 pairs holding the exact values 1024 + n (bits 0-3, 16-19 of the
   // word, and of the word >> 8) or 64 + n (bits 4-7, 20-23), n = stored nibble ^ 8 = q + 8, one v_bitop3 each:
   // ((w ^ 0x8..8) & mask) | magic. Their dot products with the fp16 high and low parts of x (v_dot2_f32_f16: exact
@@ -164,7 +151,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   // kDeep reads W and scales and writes y through buffer resources: a chunk past the wave's last row block, a tail
   // lane past K, or a lane that stores nothing issues its instruction with an out-of-range offset (no traffic, no
   // branch). Every chunk is then the same 2R loads, so the compiler's wait counts see the full pipeline depth.
-  const int wrows = MODE == kGateUp ? 2 * f : n_out;
+  const int wrows = MODE == kGateUp ? 2 * f : MODE == kMoeGateUp ? moe.experts * 2 * f : n_out;
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)wrows * kw * 4));
   // scales are read as the aligned 4 bytes holding them (a 16-bit load would be widened right after it, waiting for
   // it); the range is rounded up to whole 4-byte words, so an odd count's last scale is read with the 2 bytes after it
@@ -176,11 +163,13 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     const bool ok = ib < n_out && c < (uint32_t)nch;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t row = gemv_row<MODE, RO>(ib, r, n_out, f, moe);  // a valid row even past the end
+      const int grow = gemv_row<MODE, RO>(ib, r, n_out, f, moe);  // a valid row even past the end (-1: no expert)
+      const bool okr = ok && (MODE != kMoeGateUp || grow >= 0);   // no expert: zero words and scales
+      const uint32_t row = (uint32_t)grow;
       const uint32_t wo = (row * (uint32_t)kw + 4 * c) * 4;
       const uint32_t si = row * (uint32_t)gpr + ((32 * c) >> gsh);
-      w[r] = buf_load16p<kWPolicy>(w_rsrc, ok ? wo : kOOB);
-      sc[r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, ok ? (si * 2) & ~3u : kOOB, 0, 0);
+      w[r] = buf_load16p<kWPolicy>(w_rsrc, okr ? wo : kOOB);
+      sc[r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, okr ? (si * 2) & ~3u : kOOB, 0, 0);
       sb[r] = (si & 1) << 4;
     }
     if (ib < n_out && ++ic == cpl) ic = 0, ib += stride;
@@ -228,16 +217,6 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   if constexpr (kDeep) {
 #pragma unroll
     for (int d = 0; d < D; ++d) issue_next(wd[d], sd[d], sh[d]);
-  }
-  uint4 wa[R], wb[R];
-  uint16_t sa[R], sb[R];
-  if constexpr (kPipe) {
-    if (base0 < n_out && lane < nch) {
-      int rows0[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) rows0[r] = gemv_row<MODE, RO>(base0, r, n_out, f, moe);
-      load_chunk(rows0, lane, wa, sa);
-    }
   }
 
   // Stage x in one pass. With a norm, x * norm_w is staged and sum(x^2) gathered on the way; the row sums are then
@@ -457,23 +436,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
 
-    if constexpr (kPipe) {
-      int rw[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) rw[r] = rows[r][0];
-      if (base != base0 && lane < nch) load_chunk(rw, lane, wa, sa);  // the first block's came before staging
-      // two register sets used in turn by name (a copy of a set still in flight would wait for it)
-      for (int c = lane; c < nch; c += 2 * kWave) {
-        const bool more1 = c + kWave < nch;
-        if (more1) load_chunk(rw, c + kWave, wb, sb);
-        use_chunk(c, wa, sa, acc);
-        if (!more1) break;
-        const bool more2 = c + 2 * kWave < nch;
-        if (more2) load_chunk(rw, c + 2 * kWave, wa, sa);
-        use_chunk(c + kWave, wb, sb, acc);
-        if (!more2) break;
-      }
-    } else {
+    {
       for (int c = lane; c < nch; c += kWave) {
         if constexpr (MODE == kMoeDown) {
           // one row per expert slot t, applied to that slot's activations only. Every slot's 16 bytes (and scale)
@@ -613,7 +576,7 @@ static int launch_x(const uint32_t* wq, const uint16_t* ws, const float* x, floa
 template <bool G32, int R, int T, int MODE>
 static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
                     int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
-  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp);
+  constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp || MODE == kMoeGateUp);
   if constexpr (kDeep) {
     constexpr int RO = MODE == kGateUp ? R / 2 : R;
     const int64_t waves = 4 * (int64_t)gemv_blocks(n_out, RO);
