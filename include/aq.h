@@ -113,15 +113,18 @@ int aq_moe_route_pack(const float* logits, int32_t* ids, float* weights, int64_t
  * exclusive prefix sum of the counts padded to multiples of tm (offs[experts] = rows used); slot[i] = grouped row
  * (ascending i within an expert); src[row] = token (-1 on padding and unused rows < max_rows); work tiles (e, row)
  * every tm rows of each expert, in expert order, and their number ntiles[0]. max_rows >= aq_moe_group_max_rows,
- * max_tiles >= aq_moe_group_max_tiles. Replaces: p_group (lfm2moe/kernels/mk.mojo:123-161). */
+ * max_tiles >= aq_moe_group_max_tiles. A token may name one expert more than once: every entry is counted and
+ * entries of one expert keep ascending i (a slower ordered scan then runs in the same launch); an id outside
+ * [0, experts) gets slot -1. Replaces: p_group (lfm2moe/kernels/mk.mojo:123-161). */
 int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm, int32_t* counts,
                  int32_t* offs, int32_t* slot, int32_t* src, int64_t max_rows, int32_t* tiles, int32_t max_tiles,
                  int32_t* ntiles, void* stream);
 int64_t aq_moe_group_max_rows(int64_t tokens, int32_t topk, int32_t experts, int32_t tm);
 int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t experts, int32_t tm);
 
-/* Per-expert lists of entries: lists[e*cap + r] = the r-th entry i (ascending) with ids[i] == e, counts[e]; with
- * items != NULL also the work items (e, c) for c = 0, items_tt, ... < counts[e] in expert order and nitems[0].
+/* Per-expert lists of entries: lists[e*cap + r] = the r-th entry i (ascending, repeated ids included) with
+ * ids[i] == e, counts[e]; with items != NULL also the work items (e, c) for c = 0, items_tt, ... < counts[e] in expert
+ * order and nitems[0].
  * scratch: >= (experts + 1) + 4 * tokens * topk + 1 ints of device memory. Replaces: p_expert_lists and
  * p_expert_items (qwen3moe/kernels/moek.mojo:432-442,548-557; cap = PMAX there). */
 int aq_moe_expert_lists(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t cap,

@@ -349,7 +349,6 @@ def _moe_group_impl(ids, experts, tm, counts, offs, slot, src, tiles, ntiles):
 
 
 def _moe_gemm_q4_impl(x, src, wq, ws, experts, group, tiles, ntiles, tm, swiglu, out):
-    _dev(x, wq, ws, tiles, ntiles, out)
     _u32(wq, "wq")
     _f16bits(ws, "ws")
     _i32(tiles, ntiles)
@@ -359,10 +358,13 @@ def _moe_gemm_q4_impl(x, src, wq, ws, experts, group, tiles, ntiles, tm, swiglu,
     _check(rows % experts == 0, "wq rows must be experts * n")
     n = rows // experts
     _check(x.dim() == 2 and x.shape[1] == k, "x must be [rows, K]")
+    _check(group > 0 and k % group == 0 and ws.numel() == rows * (k // group), "ws must be [experts * n, K/group]")
+    _check(out.dim() == 2, "out must be [rows_total, n] (or [rows_total, n/2] with swiglu)")
     if swiglu:
         _check(out.dtype == torch.float16 and out.shape[1] == n // 2, "swiglu out must be float16 [rows_total, n/2]")
     else:
         _check(out.dtype == torch.float32 and out.shape[1] == n, "out must be float32 [rows_total, n]")
+    _dev(x, wq, ws, tiles, ntiles, out)
     src_ptr = 0
     if src.numel():
         _dev(src)
@@ -374,34 +376,59 @@ def _moe_gemm_q4_impl(x, src, wq, ws, experts, group, tiles, ntiles, tm, swiglu,
 
 
 def _moe_combine_impl(yd, slot, weights, y, add):
-    _dev(yd, weights, y)
-    _check(yd.dtype == torch.float32 and y.dtype == torch.float32 and weights.dtype == torch.float32, "float32")
+    # shapes and dtypes first: the kernel writes tokens * d floats of y and reads rows of yd through slot
+    _check(yd.dtype == torch.float32 and y.dtype == torch.float32 and weights.dtype == torch.float32,
+           "yd, weights and y must be float32")
+    _check(weights.dim() == 2, "weights must be [T, topk]")
     t, k = weights.shape
     d = y.shape[-1]
+    _check(y.numel() == t * d, "y must be [T, d]")
+    _check(yd.dim() == 2 and yd.shape[1] == d, "yd must be [rows, d]")
+    if slot.numel():
+        _i32(slot)
+        _check(slot.numel() == t * k, "slot must hold T * topk entries")
+    _dev(yd, weights, y)
     slot_ptr = 0
     if slot.numel():
-        _dev(slot)
-        _i32(slot)
+        _dev(yd, slot)
         slot_ptr = _ptr(slot)
     _lib.call("aq_moe_combine", _ptr(yd), yd.shape[0], slot_ptr, _ptr(weights), _ptr(y), t, d, k, int(add),
               _stream(y))
 
 
 def _moe_gate_up_q4_impl(wq, ws, experts, ids, x, a, group):
-    _dev(wq, ws, ids, x, a)
+    # shapes and dtypes first: the kernel writes topk * f floats of a
+    _u32(wq, "wq")
+    _f16bits(ws, "ws")
     _i32(ids)
+    _check(wq.dim() == 2 and experts > 0 and wq.shape[0] % (2 * experts) == 0, "wq must be [experts * 2f, K/8]")
     rows, kw = wq.shape
-    f = rows // experts // 2
-    _lib.call("aq_moe_gate_up_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(x), _ptr(a), f, kw * 8, group,
-              ids.numel(), _stream(x))
+    f, k = rows // experts // 2, kw * 8
+    _check(group > 0 and k % group == 0 and ws.numel() == rows * (k // group), "ws must be [experts * 2f, K/group]")
+    topk = ids.numel()
+    _check(x.dtype == torch.float32 and x.numel() == k, "x must be float32 [K]")
+    _check(a.dtype == torch.float32 and a.numel() == topk * f, "a must be float32 [topk, f]")
+    _dev(wq, ws, ids, x, a)
+    _lib.call("aq_moe_gate_up_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(x), _ptr(a), f, k, group, topk,
+              _stream(x))
 
 
 def _moe_down_q4_impl(wq, ws, experts, ids, weights, a, y, group, add):
-    _dev(wq, ws, ids, weights, a, y)
+    # shapes and dtypes first: the kernel writes d floats of y
+    _u32(wq, "wq")
+    _f16bits(ws, "ws")
     _i32(ids)
+    _check(wq.dim() == 2 and experts > 0 and wq.shape[0] % experts == 0, "wq must be [experts * d, f/8]")
     rows, kw = wq.shape
-    _lib.call("aq_moe_down_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(weights), _ptr(a), _ptr(y),
-              rows // experts, kw * 8, group, ids.numel(), int(add), _stream(y))
+    d, f = rows // experts, kw * 8
+    _check(group > 0 and f % group == 0 and ws.numel() == rows * (f // group), "ws must be [experts * d, f/group]")
+    topk = ids.numel()
+    _check(weights.dtype == torch.float32 and weights.numel() == topk, "weights must be float32 [topk]")
+    _check(a.dtype == torch.float32 and a.numel() == topk * f, "a must be float32 [topk, f]")
+    _check(y.dtype == torch.float32 and y.numel() == d, "y must be float32 [d]")
+    _dev(wq, ws, ids, weights, a, y)
+    _lib.call("aq_moe_down_q4", _ptr(wq), _ptr(ws), experts, _ptr(ids), _ptr(weights), _ptr(a), _ptr(y), d, f,
+              group, topk, int(add), _stream(y))
 
 
 def _gemv_f32_impl(w, x, y):

@@ -421,8 +421,9 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
   if (m <= 0 || n <= 0 || k <= 0 || k % (FMT == kT2 ? 128 : 32)) return AQ_ERR_SHAPE;
   if (m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return AQ_ERR_SHAPE;
   if (FMT == kQ4 && (group <= 0 || group % 8 || k % group)) return AQ_ERR_GROUP;
-  // buffer offsets are 32-bit: each operand must stay under 2 GiB
-  if (m * k * (xf32 ? 4 : 2) >= ((int64_t)1 << 31) || n * k / (FMT == kT2 ? 4 : 2) >= ((int64_t)1 << 31))
+  // buffer offsets are 32-bit: each operand (X, W, Y and each split's partial slab of M x N floats) stays under 2 GiB
+  if (m * k * (xf32 ? 4 : 2) >= ((int64_t)1 << 31) || n * k / (FMT == kT2 ? 4 : 2) >= ((int64_t)1 << 31) ||
+      m * n * 4 >= ((int64_t)1 << 31))
     return AQ_ERR_CAPACITY;
   if (!aligned(wq, 16) || !aligned(x, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

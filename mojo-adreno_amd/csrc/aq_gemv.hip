@@ -578,7 +578,7 @@ static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, floa
                     int f, int tokens, const MoeArgs& moe, const Fuse& fz, hipStream_t s) {
   constexpr bool kDeep = G32 && (MODE == kStore || MODE == kAdd || MODE == kGateUp || MODE == kMoeGateUp);
   if constexpr (kDeep) {
-    constexpr int RO = MODE == kGateUp ? R / 2 : R;
+    constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
     const int64_t waves = 4 * (int64_t)gemv_blocks(n_out, RO);
     const int64_t items = ((k / 32 + 63) / 64) * ((n_out + waves * RO - 1) / (waves * RO));
     if (items >= 4 && R <= 2) return launch_x<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
@@ -694,6 +694,9 @@ extern "C" int aq_moe_gate_up_q4(const uint32_t* wq, const uint16_t* ws, int64_t
                                  void* stream) {
   if (!ids) return AQ_ERR_NULL;
   if (topk <= 0 || f <= 0 || experts <= 0 || topk * f > (1 << 30) || experts * 2 * f > INT32_MAX) return AQ_ERR_SHAPE;
+  // the kernel reads the stacked experts' rows through one buffer resource with 32-bit offsets (their scales, at
+  // group >= 8, take fewer bytes than the words)
+  if (k > 0 && experts * 2 * f * (k / 2) >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
   const aq::MoeArgs moe{ids, nullptr, (int)experts, 0};
   return aq::gemv_entry<aq::kMoeGateUp>(wq, ws, x, a, topk * f, k, group, f, 1, moe, stream);
 }

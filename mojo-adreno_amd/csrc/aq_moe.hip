@@ -80,8 +80,11 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
 // (e, offs[e] + c) for c = 0, tm, ... < cnt[e], in expert order, and their number. Optionally the qwen3moe lists
 // (lists[e * cap + r] = i of rank r) and items ((e, c) every `items_tt` entries).
 // Ranks without atomics deciding any order: bit t of expert e's token bitmap is set (LDS atomic OR, order-free) when
-// token t chose e; a token chooses an expert at most once (top-k of distinct experts), so the rank of entry i is the
-// number of set bits below t: a per-word prefix popcount plus the popcount of the bits below t in its word.
+// token t chose e. While a token chooses an expert at most once (top-k of distinct experts), the rank of entry i is
+// the number of set bits below t: a per-word prefix popcount plus the popcount of the bits below t in its word. An
+// OR that finds its bit already set shows a token that chose one expert twice; the whole launch then takes the
+// reference's ordered scan instead (p_group: one thread per expert walks the entries in ascending i, here in chunks
+// staged in LDS), which counts every entry and ranks repeated ones in ascending i.
 struct GroupOut {
   int32_t* counts;   // [E]
   int32_t* offs;     // [E + 1]
@@ -95,6 +98,8 @@ struct GroupOut {
   int cap, items_tt, max_rows, max_tiles, max_items;
 };
 
+constexpr int kGroupChunk = 1024;  // entries staged per round of the ordered scan
+
 __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ ids, int n, int topk, int E, int tm,
                                                     GroupOut o) {
   extern __shared__ unsigned long long bits[];  // [E][W] token bitmaps
@@ -104,25 +109,49 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
   int32_t* eoff = pre + E * W;   // [E + 1] first row of expert e's segment
   int32_t* tbase = eoff + E + 1; // [E + 1] first work tile of expert e
   int32_t* ibase = tbase + E + 1;// [E + 1] first work item of expert e (lists mode)
+  int32_t* chunk = ibase + E + 1;// [kGroupChunk] entries of one round of the ordered scan
   __shared__ int32_t wtot[16][3];
+  __shared__ int repeated;       // some token chose one expert twice: ordered scan
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) repeated = 0;
   for (int i = threadIdx.x; i < E * W; i += 1024) bits[i] = 0ull;
   for (int r = threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;  // padding rows; real rows are set below
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += 1024) {
     const int e = ids[i];
-    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * W + ((i / topk) >> 6)], 1ull << ((i / topk) & 63));
+    if (e >= 0 && e < E) {
+      const unsigned long long bit = 1ull << ((i / topk) & 63);
+      if (atomicOr(&bits[(size_t)e * W + ((i / topk) >> 6)], bit) & bit) repeated = 1;
+    }
   }
   __syncthreads();
+  const bool scan = repeated != 0;  // workgroup-uniform
+  const int e = threadIdx.x;
+  // The ordered scan: every thread stages the entries [base, base + kGroupChunk) into LDS, then thread e (< E) walks
+  // them in ascending i and calls visit(i) for each entry of its expert. Barriers are workgroup-uniform.
+  auto ordered_scan = [&](auto visit) {
+    for (int base = 0; base < n; base += kGroupChunk) {
+      const int len = min(kGroupChunk, n - base);
+      for (int j = threadIdx.x; j < len; j += 1024) chunk[j] = ids[base + j];
+      __syncthreads();
+      if (e < E)
+        for (int j = 0; j < len; ++j)
+          if (chunk[j] == e) visit(base + j);
+      __syncthreads();
+    }
+  };
   // one thread per expert: count, padded rows, tiles, items; then exclusive scans over the experts (16 waves x 64)
   int c = 0, rows = 0, nt = 0, ni = 0;
-  const int e = threadIdx.x;
-  if (e < E) {
+  if (scan) {
+    ordered_scan([&](int) { ++c; });
+  } else if (e < E) {
     for (int w = 0; w < W; ++w) {
       pre[e * W + w] = c;
       c += __popcll(bits[(size_t)e * W + w]);
     }
+  }
+  if (e < E) {
     nt = (c + tm - 1) / tm;
     rows = nt * tm;
     ni = o.items ? (c + o.items_tt - 1) / o.items_tt : 0;
@@ -173,19 +202,27 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
     }
   }
   __syncthreads();
+  // entry i of expert ex at rank r among ex's entries
+  auto place = [&](int i, int ex, int rank) {
+    const int row = eoff[ex] + rank;
+    o.slot[i] = row;
+    if (row < o.max_rows) o.src[row] = i / topk;
+    if (o.lists && rank < o.cap) o.lists[(size_t)ex * o.cap + rank] = i;
+  };
   for (int i = threadIdx.x; i < n; i += 1024) {
     const int ex = ids[i];
     if (ex < 0 || ex >= E) {
       o.slot[i] = -1;  // an id outside [0, E) is in no group
       continue;
     }
+    if (scan) continue;  // placed by the ordered scan below
     const int t = i / topk;
     const unsigned long long word = bits[(size_t)ex * W + (t >> 6)];
-    const int rank = pre[ex * W + (t >> 6)] + __popcll(word & ((1ull << (t & 63)) - 1ull));
-    const int row = eoff[ex] + rank;
-    o.slot[i] = row;
-    if (row < o.max_rows) o.src[row] = t;
-    if (o.lists && rank < o.cap) o.lists[(size_t)ex * o.cap + rank] = i;
+    place(i, ex, pre[ex * W + (t >> 6)] + __popcll(word & ((1ull << (t & 63)) - 1ull)));
+  }
+  if (scan) {
+    int rank = 0;
+    ordered_scan([&](int i) { place(i, e, rank++); });
   }
 }
 
@@ -282,7 +319,7 @@ extern "C" int32_t aq_moe_group_max_tiles(int64_t tokens, int32_t topk, int32_t 
 
 static size_t group_lds(int64_t tokens, int E) {
   const int64_t W = (tokens + 63) / 64;
-  return (size_t)E * W * 12 + (size_t)3 * (E + 1) * 4;
+  return (size_t)E * W * 12 + (size_t)3 * (E + 1) * 4 + (size_t)aq::kGroupChunk * 4;
 }
 
 extern "C" int aq_moe_group(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t tm,

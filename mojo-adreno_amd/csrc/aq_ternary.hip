@@ -5,11 +5,16 @@
 // bonsai/kernels/kernels.mojo:189-325 (``_group_dot8`` / ``packed_linear``) and :437-448 (``packed_reduce``); the
 // reference accumulates each group in fp16 chains, this build decodes exactly and accumulates in fp32.
 //
-// Decode (HBM-bound: 0.27 B per weight, so ~1.5 VALU ops per weight is the budget). For code position j <= 4 of a
-// 16-bit half, (word & (0x00030003 << 2j)) | 0x64006400 is the fp16 pair (1024 + c_j * 4^j, 1024 + c_{j+8} * 4^j)
-// exactly (the code lands in mantissa bits 2j, 2j+1); subtracting 1024 + 4^j leaves (c - 1) * 4^j exactly, and
-// v_dot2_f32_f16 against the x pair pre-scaled by 4^-j accumulates (c - 1) * x in fp32 with exact products. Positions
-// 5..7 are the same after one shift by 10. That is 25 VALU ops per 16 weights, no table and no bias to cancel.
+// Decode (HBM-bound: 0.27 B per weight, so ~1.5 VALU ops per weight is the budget). Two forms:
+// - biased (t2_word_dot_b; the GEMVs k_t2_gemv_cols and k_t2_gemv_wide, and so the output head): four shifts of the
+//   word bring each pair of code positions to bits 6-9 of both halves, one v_bitop3 per pair fills the rest with the
+//   exponent of 16.0 or 4.0, giving the exact fp16 pair (B + c, B + c'); v_dot2_f32_f16 with the unscaled x pair sums
+//   (B + c) x with exact products, and a per-128-group bias sum (B + 1) x, staged with x, is subtracted. 56 issue
+//   cycles per 16 weights.
+// - exact (t2_word_dot; k_t2_partials, the packed_linear drop-in): for code position j <= 4 of a 16-bit half,
+//   (word & (0x00030003 << 2j)) | 0x64006400 is the fp16 pair (1024 + c_j * 4^j, 1024 + c_{j+8} * 4^j); subtracting
+//   1024 + 4^j leaves (c - 1) * 4^j exactly, and v_dot2_f32_f16 against the x pair pre-scaled by 4^-j accumulates
+//   (c - 1) * x in fp32. Positions 5..7 are the same after one shift by 10. No bias to cancel.
 #include "aq_common.h"
 
 namespace aq {

@@ -26,7 +26,8 @@ Pinning status (how each function is checked, see tests/test_oracle_*.py):
     reference sources by oracle/Makefile: golden vectors in tests/golden/ref_*.npz (zero groups, .5 ties, fp16
     subnormals, negative maxima) and, where oracle/_ref is built, fresh runs of the binaries
     (tests/test_oracle_golden.py). Also ggml's published Q4_0 block layout, re-derived independently.
-  * mlx_to_t2w: MLX's published 2-bit affine layout (weight = code*scale + bias), checked by dequantising both sides.
+  * mlx_to_t2w: MLX's published 2-bit affine layout (weight = code*scale + bias): its T2W output, dequantised, equals a
+    pure-Python bit walk of the MLX input (tests/test_formats.py::test_t2w_from_mlx_closed_form).
 The exact fp32 bits of the reference's Mojo kernels (its reduction order and MAX's warp/coop-matrix primitives)
 cannot be reproduced here: that part is "parity unpinned" and parity is defined by tolerance.
 """
@@ -44,10 +45,15 @@ def q4w_values(wq: np.ndarray) -> np.ndarray:
 
     Follows llama/kernels/gemv_q4.mojo:24-26 and qwen3moe/reference.py:62-63. Returns int8 [..., 8*W].
     """
-    wq = np.asarray(wq, dtype=np.uint32)
-    nib = (wq[..., None] >> (np.arange(8, dtype=np.uint32) * 4)) & np.uint32(15)
-    vals = (nib.astype(np.int16) ^ 8) - 8
-    return vals.reshape(*wq.shape[:-1], wq.shape[-1] * 8).astype(np.int8)
+    wq = np.ascontiguousarray(np.asarray(wq, dtype="<u4"))  # little-endian: byte b of a word holds nibbles 2b, 2b+1
+    b = wq.view(np.uint8)
+    nib = np.empty(b.shape + (2,), np.uint8)
+    np.bitwise_and(b, 15, out=nib[..., 0])
+    np.right_shift(b, 4, out=nib[..., 1])
+    nib ^= 8
+    vals = nib.view(np.int8)
+    vals -= 8
+    return vals.reshape(*wq.shape[:-1], wq.shape[-1] * 8)
 
 
 def q4w_pack(q: np.ndarray) -> np.ndarray:
@@ -392,10 +398,13 @@ class LlamaDecodeOracle:
 
     ``arrays`` as ``aq.llama.LlamaWeights.from_numpy`` takes them; ``cos``/``sin`` [max_pos, d/2] tables."""
 
-    def __init__(self, arrays: dict, cfg, cos, sin, kv_dtype=np.float16):
+    def __init__(self, arrays: dict, cfg, cos, sin, kv_dtype=np.float16, weights_dtype=np.float64):
         self.cfg, self.cos, self.sin, self.kv_dtype = cfg, np.asarray(cos), np.asarray(sin), kv_dtype
         g = cfg.group
-        deq = lambda name: q4w_dequant(arrays[name + ".q"], arrays[name + ".s"], g).astype(np.float64)  # noqa: E731
+        # the dequantised weights are exact in float32 (int4 times fp16); float32 storage halves the memory of a
+        # whole-depth model and changes no product, since every matrix-vector product is taken in float64 (_mv)
+        deq = lambda name: q4w_dequant(arrays[name + ".q"], arrays[name + ".s"], g).astype(weights_dtype,  # noqa: E731
+                                                                                       copy=False)
         self.embed = np.asarray(arrays["embed"], dtype=np.float16)
         self.layers = []
         for i in range(cfg.layers):
@@ -412,23 +421,30 @@ class LlamaDecodeOracle:
     def _store(self, v):
         return v.astype(self.kv_dtype).astype(np.float64) if self.kv_dtype is not None else v
 
+    @staticmethod
+    def _mv(w, x):
+        """w @ x in float64, in row blocks (a float32 w is widened one block at a time)."""
+        if w.dtype == np.float64:
+            return w @ x
+        return np.concatenate([w[r:r + 4096].astype(np.float64) @ x for r in range(0, w.shape[0], 4096)])
+
     def step(self, token: int, pos: int) -> np.ndarray:
         """Logits (float64 [vocab]) of ``token`` at ``pos``; appends this position's keys and values to the cache."""
         cfg = self.cfg
         hd, nh, nkv = cfg.head_dim, cfg.heads, cfg.kv_heads
         x = self.embed[token].astype(np.float64)
         for i, lw in enumerate(self.layers):
-            qkv = lw["wqkv"] @ rmsnorm(x, lw["attn_norm"], cfg.eps)
+            qkv = self._mv(lw["wqkv"], rmsnorm(x, lw["attn_norm"], cfg.eps))
             q = rope(qkv[:nh * hd].reshape(nh, hd), self.cos[pos], self.sin[pos])
             k = rope(qkv[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), self.cos[pos], self.sin[pos])
             v = qkv[(nh + nkv) * hd:].reshape(nkv, hd)
             self.kc[i][:, pos] = self._store(k)
             self.vc[i][:, pos] = self._store(v)
             att = attention_decode(q, self.kc[i], self.vc[i], pos + 1)
-            x = x + lw["wo"] @ att.reshape(-1)
-            h = lw["wgu"] @ rmsnorm(x, lw["mlp_norm"], cfg.eps)
-            x = x + lw["wdown"] @ (silu(h[:cfg.ffn]) * h[cfg.ffn:])
-        return self.lm @ rmsnorm(x, self.final_norm, cfg.eps)
+            x = x + self._mv(lw["wo"], att.reshape(-1))
+            h = self._mv(lw["wgu"], rmsnorm(x, lw["mlp_norm"], cfg.eps))
+            x = x + self._mv(lw["wdown"], silu(h[:cfg.ffn]) * h[cfg.ffn:])
+        return self._mv(self.lm, rmsnorm(x, self.final_norm, cfg.eps))
 
 
 # ----------------------------------------------------------------------------------------------------------------

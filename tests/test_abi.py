@@ -163,3 +163,83 @@ def test_moe_route_pack_validation():
     assert lib.aq_moe_route_pack(p, p, p, 4, 128, 8, p, p, 2044, None) == 1       # d % 8
     assert lib.aq_moe_route_pack(p, p, p, 4, 300, 8, p, p, 2048, None) == 1       # experts > 256
     assert lib.aq_moe_route_pack(p, p, p, 4, 128, 8, p + 4, p, 2048, None) == 3   # x not 16-byte aligned
+
+
+def test_operand_size_guards():
+    """Operands addressed through one 32-bit buffer range are refused (AQ_ERR_CAPACITY) at 2 GiB and above."""
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    # MoE decode gate|up: the stacked experts' rows, experts * 2f * K/2 bytes
+    assert lib.aq_moe_gate_up_q4(p, p, 1024, p, p, p, 1024, 2048, 32, 8, None) == 6   # exactly 2 GiB
+    assert lib.aq_moe_gate_up_q4(p, p, 1023, p, p, p, 1024, 2048, 32, 8, None) != 6   # just below (fails later)
+    assert lib.aq_moe_down_q4(p, p, 1024, p, p, p, p, 2048, 2048, 32, 8, 0, None) == 6
+    # dense GEMM: Y (and each split's partial slab) is M x N floats
+    assert lib.aq_gemm_q4(p, 0, p, p, p, 4096, 131072, 128, 32, 0, None, 0, None) == 6
+    assert lib.aq_gemm_t2(p, 0, p, p, p, 4096, 131072, 128, 0, None, 0, None) == 6
+    assert lib.aq_gemm_q4(p, 0, p, p, p, 4095, 131072, 128, 32, 0, None, 0, None) != 6
+
+
+def _moe_decode_tensors(experts=4, f=64, d=64, k=64, topk=2, group=32):
+    import torch
+    i32 = torch.int32
+    return dict(
+        gu_q=torch.zeros((experts * 2 * f, k // 8), dtype=i32), gu_s=torch.zeros((experts * 2 * f, k // group),
+                                                                                  dtype=torch.float16),
+        dn_q=torch.zeros((experts * d, f // 8), dtype=i32), dn_s=torch.zeros((experts * d, f // group),
+                                                                             dtype=torch.float16),
+        ids=torch.zeros(topk, dtype=i32), w=torch.zeros(topk), x=torch.zeros(k), a=torch.zeros((topk, f)),
+        y=torch.zeros(d), experts=experts, group=group)
+
+
+def _raises(fn, match):
+    with pytest.raises(ValueError, match=match):
+        fn()
+
+
+def test_moe_decode_ops_validate_shapes_before_launch():
+    """The MoE decode wrappers check every shape and dtype before any launch: mis-sized outputs are refused on the host
+    (with host tensors the checks pass only to stop at the device check)."""
+    import torch
+    from aq import ops
+    t = _moe_decode_tensors()
+    gu = lambda **o: (lambda: ops._moe_gate_up_q4_impl(o.get("wq", t["gu_q"]), o.get("ws", t["gu_s"]), t["experts"],
+                                                        o.get("ids", t["ids"]), o.get("x", t["x"]), o.get("a", t["a"]),
+                                                        t["group"]))
+    _raises(gu(), "device")
+    _raises(gu(a=torch.zeros((2, 65))), "a must be")
+    _raises(gu(a=torch.zeros((2, 64), dtype=torch.float16)), "a must be")
+    _raises(gu(x=torch.zeros(63)), "x must be")
+    _raises(gu(ws=torch.zeros((4 * 128, 1), dtype=torch.float16)), "ws must be")
+    _raises(gu(wq=torch.zeros((4 * 128 + 2, 8), dtype=torch.int32)), "wq must be")
+    _raises(gu(ids=torch.zeros(2, dtype=torch.int64)), "int32")
+    dn = lambda **o: (lambda: ops._moe_down_q4_impl(o.get("wq", t["dn_q"]), o.get("ws", t["dn_s"]), t["experts"],
+                                                     o.get("ids", t["ids"]), o.get("w", t["w"]), o.get("a", t["a"]),
+                                                     o.get("y", t["y"]), t["group"], False))
+    _raises(dn(), "device")
+    _raises(dn(y=torch.zeros(65)), "y must be")
+    _raises(dn(a=torch.zeros((3, 64))), "a must be")
+    _raises(dn(w=torch.zeros(3)), "weights must be")
+    _raises(dn(ws=torch.zeros((256, 3), dtype=torch.float16)), "ws must be")
+
+
+def test_moe_combine_and_gemm_validate_shapes_before_launch():
+    import torch
+    from aq import ops
+    yd, slot, w, y = torch.zeros((16, 32)), torch.zeros(8, dtype=torch.int32), torch.zeros((4, 2)), torch.zeros((4, 32))
+    cb = lambda **o: (lambda: ops._moe_combine_impl(o.get("yd", yd), o.get("slot", slot), o.get("w", w),
+                                                    o.get("y", y), False))
+    _raises(cb(), "device")
+    _raises(cb(y=torch.zeros((5, 32))), "y must be")
+    _raises(cb(yd=torch.zeros((16, 36))), "yd must be")
+    _raises(cb(slot=torch.zeros(7, dtype=torch.int32)), "slot must")
+    _raises(cb(w=torch.zeros(8)), "weights must be")
+    x = torch.zeros((4, 64), dtype=torch.float16)
+    wq, ws = torch.zeros((2 * 32, 8), dtype=torch.int32), torch.zeros((2 * 32, 2), dtype=torch.float16)
+    tiles, nt, out = torch.zeros(8, dtype=torch.int32), torch.zeros(1, dtype=torch.int32), torch.zeros((48, 32))
+    gm = lambda **o: (lambda: ops._moe_gemm_q4_impl(x, torch.zeros(0, dtype=torch.int32), wq, o.get("ws", ws), 2, 32,
+                                                    tiles, nt, 16, False, o.get("out", out)))
+    _raises(gm(), "device")
+    _raises(gm(ws=torch.zeros((64, 1), dtype=torch.float16)), "ws must be")
+    _raises(gm(out=torch.zeros((48, 31))), "out must be")

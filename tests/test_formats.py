@@ -131,6 +131,48 @@ def test_t2w_from_mlx_vs_oracle(fmt):
     np.testing.assert_array_equal(_u16(s), _u16(s_ref))
 
 
+def _mlx_affine_dequant(codes, scales, biases, k):
+    """MLX's published 2-bit affine format (mlx.core.quantize with bits = 2, group_size = 128, the quantisation
+    qwen3/export.py:41 asserts): element k of row n is bits 2 (k % 16) of word k / 16 (16 codes per uint32, lowest
+    bits first) and its value is code * scales[n, k/128] + biases[n, k/128]. A pure-Python bit walk in float64,
+    independent of both converters."""
+    n = codes.shape[0]
+    out = np.zeros((n, k))
+    for r in range(n):
+        for kk in range(k):
+            code = (int(codes[r, kk // 16]) >> (2 * (kk % 16))) & 3
+            out[r, kk] = code * float(scales[r, kk // 128]) + float(biases[r, kk // 128])
+    return out
+
+
+def test_t2w_from_mlx_closed_form(fmt):
+    """Pins the MLX -> T2W converter (qwen3/convert.cpp:39-74) to MLX's own dequantisation: the fused T2W matrix,
+    dequantised as T2W ((code - 1) * s), equals every part's MLX value code * scale + bias stacked along N, for the
+    library's C++ and the oracle alike. Codes cover 0..3 (3 is 2 * scale when bias = -scale). A planted swap of two
+    parts and an untransposed word layout both fail the same check."""
+    rng = np.random.default_rng(13)
+    k = 256
+    parts, mlx = [], []
+    for n in (24, 8, 40):
+        codes = rng.integers(0, 2 ** 32, size=(n, k // 16), dtype=np.uint32)
+        sc = (np.abs(rng.standard_normal((n, k // 128))) * 0.02).astype(np.float16)
+        bi = (-sc.astype(np.float32)).astype(np.float16)
+        parts.append((codes, sc, bi))
+        mlx.append(_mlx_affine_dequant(codes, sc, bi, k))
+    want = np.concatenate(mlx, axis=0)  # [sum n, K]
+
+    def matches(w, s):
+        return w.shape == (k // 16, want.shape[0]) and np.array_equal(orc.t2w_dequant(w, s).astype(np.float64), want)
+
+    assert matches(*fmt.t2w_from_mlx(parts, k))
+    assert matches(*orc.mlx_to_t2w(parts, k))
+    # planted mistakes the check must catch
+    assert not matches(*orc.mlx_to_t2w([parts[1], parts[0], parts[2]], k))     # parts in the wrong order
+    w, s = orc.mlx_to_t2w(parts, k)
+    flat = np.concatenate([c for c, _, _ in parts], axis=0)                     # codes left [N, K/16] row-major
+    assert not matches(np.ascontiguousarray(flat.reshape(k // 16, -1)), s)      # ... read as if transposed
+
+
 def test_t2w_from_mlx_rejects_non_ternary(fmt):
     from aq import AqError
     k = 256

@@ -201,8 +201,9 @@ def _decoder(cfg, seed, dev):
     return LlamaDecoder(LlamaWeights.from_numpy(cfg, arrays, dev)), orc.LlamaDecodeOracle(arrays, cfg, cos, sin)
 
 
-@pytest.mark.parametrize("cfg_kw", [{}, dict(dim=2048, heads=32, kv_heads=8, ffn=8192, vocab=32000, max_pos=512)],
-                         ids=["small", "llama1b-width-2-layers"])
+@pytest.mark.parametrize("cfg_kw", [{}, dict(dim=2048, heads=32, kv_heads=8, ffn=8192, vocab=32000, max_pos=512),
+                                    dict(dim=2048, heads=32, kv_heads=8, ffn=8192, vocab=32000, max_pos=512, group=64)],
+                         ids=["small", "llama1b-width-2-layers", "llama1b-width-2-layers-g64"])
 def test_decode_steps_vs_oracle(dev, cfg_kw):
     """Token-by-token forward steps: logits within rel 1e-3 of the float64 oracle (same fp16 cache rounding) at every
     step, and the device argmax is the first maximum of those logits.
@@ -228,6 +229,35 @@ def test_decode_steps_vs_oracle(dev, cfg_kw):
             assert rel_inf(lg, ref) < TOL, pos
         assert int(dec.token.item()) == orc.argmax_first(lg)
         assert int(dec.pos.item()) == pos + 1
+
+
+def test_decode_whole_depth_end_of_context(dev):
+    """All 16 layers at Llama-3.2-1B width (vocabulary cut to 32000) at the end of a 512-position context: both caches
+    hold the same fp16 rows 0..506, then positions 507..511 are decoded; the logits stay within rel 1e-3 of the
+    float64 oracle at every step, as the reference checks its whole-model logits (llama/run.py:186-198,295-306)."""
+    from aq import synth
+    from aq.llama import LlamaConfig, LlamaDecoder, LlamaWeights, rope_tables
+    cfg = LlamaConfig(vocab=32000)
+    assert cfg.layers == 16 and cfg.max_pos == 512
+    arrays = synth.llama_arrays(cfg, 23)
+    arrays["embed"] = (arrays["embed"].astype(np.float32) * 0.1).astype(np.float16)
+    dec = LlamaDecoder(LlamaWeights.from_numpy(cfg, arrays, dev))
+    oracle = orc.LlamaDecodeOracle(arrays, cfg, *rope_tables(cfg), weights_dtype=np.float32)
+    del arrays
+    rng = np.random.default_rng(5)
+    p0 = 507
+    for i in range(cfg.layers):
+        kc = (rng.standard_normal((cfg.kv_heads, p0, cfg.head_dim)) * 3).astype(np.float16)
+        vc = rng.standard_normal((cfg.kv_heads, p0, cfg.head_dim)).astype(np.float16)
+        dec.kc[i][:, :p0] = to_dev(kc, dev)
+        dec.vc[i][:, :p0] = to_dev(vc, dev)
+        oracle.kc[i][:, :p0] = kc.astype(np.float64)
+        oracle.vc[i][:, :p0] = vc.astype(np.float64)
+    for pos, t in zip(range(p0, 512), [1, 500, 31999, 7, 123]):
+        lg = to_np(dec.forward(t, pos))
+        ref = oracle.step(t, pos)
+        assert rel_inf(lg, ref) < TOL, pos
+        assert int(dec.token.item()) == orc.argmax_first(lg)
 
 
 def test_generate_graph_vs_oracle_greedy(dev):

@@ -43,6 +43,28 @@ def test_kat_bit_exact(dev, n, k, group, tokens):
     np.testing.assert_array_equal(to_np(y), exact_int4_product(vals, ws, x, group).astype(np.float32))
 
 
+@pytest.mark.parametrize("n,k,group,tokens", [(8192, 2048, 32, 1), (4096, 2048, 64, 1), (2048, 8192, 32, 1),
+                                                (3000, 2048, 128, 1), (1000, 2048, 32, 4), (700, 1024, 32, 13)])
+def test_elementwise_error_bound(dev, n, k, group, tokens):
+    """Every output, not only the largest, within 1e-3 of its own scale: |y - ref| <= 1e-3 * (|W| . |x|) elementwise.
+    The power-of-two-group path sums fp16 magic-offset pairs and cancels the offsets afterwards, so x spans seven
+    decades within and across 32-wide chunks (a small x beside a large one in the same chunk keeps only its fp16
+    low part). The bound is relative to |W| . |x|, not to |y|, so it also holds the rows whose sums nearly cancel."""
+    import torch
+    from aq import synth
+    rng = np.random.default_rng(n + k + group + tokens)
+    wq, ws = synth.int4_matrix(rng, n, k, group)
+    x = (rng.standard_normal((tokens, k)) * 10.0 ** rng.uniform(-4, 3, size=(tokens, k))).astype(np.float32)
+    y = torch.empty((tokens, n), dtype=torch.float32, device=dev)
+    _ops().gemv_q4(to_dev(wq, dev), to_dev(ws, dev), to_dev(x, dev), y, group)
+    w = orc.q4w_dequant(wq, ws, group).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T
+    scale = np.abs(x.astype(np.float64)) @ np.abs(w).T
+    err = np.abs(to_np(y).astype(np.float64) - ref)
+    worst = float(np.max(err / scale))
+    assert worst <= 1e-3, worst
+
+
 @pytest.mark.parametrize("tokens", [1, 4])
 def test_add_residual(dev, tokens):
     """gemv_add_q4: y += W x (llama/kernels/gemv_add_q4.mojo:30)."""

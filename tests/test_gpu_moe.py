@@ -138,12 +138,14 @@ def _small_moe(rng, e, d, f, g, kat=False):
     return gu_q, gu_s, dn_q, dn_s, None, None
 
 
-def test_grouped_gemm_kat_exact(dev):
+@pytest.mark.parametrize("d,n,g", [(256, 96, 32), (768, 64, 128), (2048, 32, 128), (512, 48, 64)])
+def test_grouped_gemm_kat_exact(dev, d, n, g):
     """Grouped GEMM without the SwiGLU epilogue on integer-exact inputs: each grouped row equals its token's exact
-    product with its expert's matrix; padding rows are zero."""
+    product with its expert's matrix; padding rows are zero. G = 128 is qwen3moe's expert group
+    (qwen3moe/kernels/moek.mojo:26, qwen3moe/export.py:39); K = 768 is its down projection (6 groups a row)."""
     import torch
-    rng = np.random.default_rng(8)
-    t, e, k, d, n, g, tm = 60, 6, 2, 256, 96, 32, 32
+    rng = np.random.default_rng(8 + d + g)
+    t, e, k, tm = 60, 6, 2, 32
     vals, ws, _ = kat_int4(rng, e * n, d, g)
     x = rng.integers(-3, 4, size=(t, d)).astype(np.float16)
     ids = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
@@ -191,17 +193,89 @@ def test_c3_moe_block(dev, t, tm):
     assert rel_inf(to_np(out2), ref + res) < 1e-2
 
 
-def test_c3_decode_one_token(dev):
+def test_c3_moe_block_group128(dev):
+    """The C3 block at qwen3moe's own expert group, G = 128 (qwen3moe/kernels/moek.mojo:26, qwen3moe/export.py:39):
+    grouped gate|up over K = 2048 (16 groups a row) and grouped down over K = 768 (6 groups a row)."""
     import torch
     from aq import moe, synth
-    d = synth.c3(tokens=1)
+    t = 404
+    d = synth.c3(tokens=t, group=128)
     to = lambda a: to_dev(a, dev)  # noqa: E731
-    blk = moe.MoeBlock(to(d["gu_q"]), to(d["gu_s"]), to(d["dn_q"]), to(d["dn_s"]), 128, 2048, 768, 32, 8,
+    blk = moe.MoeBlock(to(d["gu_q"]), to(d["gu_s"]), to(d["dn_q"]), to(d["dn_s"]), 128, 2048, 768, 128, 8,
+                       max_tokens=512, tm=48)
+    out = torch.empty((t, 2048), dtype=torch.float32, device=dev)
+    blk.forward(to(d["x"]), to(d["logits"]), out)
+    ref, rids, _ = orc.moe_layer(d["x"], d["logits"], d["gu_q"], d["gu_s"], d["dn_q"], d["dn_s"], 128, 768)
+    np.testing.assert_array_equal(to_np(blk.ids[:t]), rids)
+    assert rel_inf(to_np(out), ref) < 1e-2
+
+
+@pytest.mark.parametrize("g", [32, 128])
+def test_c3_decode_one_token(dev, g):
+    """One token through the decode experts (route, gate|up over the 8 chosen experts, weighted down), at C0's group
+    and at qwen3moe's G = 128."""
+    import torch
+    from aq import moe, synth
+    d = synth.c3(tokens=1, group=g)
+    to = lambda a: to_dev(a, dev)  # noqa: E731
+    blk = moe.MoeBlock(to(d["gu_q"]), to(d["gu_s"]), to(d["dn_q"]), to(d["dn_s"]), 128, 2048, 768, g, 8,
                        max_tokens=1)
     out = torch.empty(2048, dtype=torch.float32, device=dev)
     blk.decode(to(d["x"][0]), to(d["logits"][0]), out)
-    ref, _, _ = orc.moe_layer(d["x"], d["logits"], d["gu_q"], d["gu_s"], d["dn_q"], d["dn_s"], 32, 768)
+    ref, _, _ = orc.moe_layer(d["x"], d["logits"], d["gu_q"], d["gu_s"], d["dn_q"], d["dn_s"], g, 768)
     assert rel_inf(to_np(out), ref[0]) < 1e-3
+
+
+@pytest.mark.parametrize("hidden,ffn,g", [(8192, 256, 32), (8192, 256, 128), (4096, 512, 64)])
+def test_moe_decode_deep_pipeline(dev, hidden, ffn, g):
+    """Decode experts at widths where the gate|up launch streams several chunks per lane through its register sets
+    (K = 8192: four chunks a row per lane, so four sets in flight; K = 4096: two), vs the oracle."""
+    import torch
+    from aq import moe, synth
+    d = synth.c3(seed=9, tokens=1, experts=16, hidden=hidden, ffn=ffn, group=g)
+    to = lambda a: to_dev(a, dev)  # noqa: E731
+    blk = moe.MoeBlock(to(d["gu_q"]), to(d["gu_s"]), to(d["dn_q"]), to(d["dn_s"]), 16, hidden, ffn, g, 8,
+                       max_tokens=1)
+    out = torch.empty(hidden, dtype=torch.float32, device=dev)
+    blk.decode(to(d["x"][0]), to(d["logits"][0]), out)
+    ref, _, _ = orc.moe_layer(d["x"], d["logits"], d["gu_q"], d["gu_s"], d["dn_q"], d["dn_s"], g, ffn)
+    assert rel_inf(to_np(out), ref[0]) < 1e-3
+
+
+@pytest.mark.parametrize("t,e,k,tm", [(50, 8, 4, 16), (404, 128, 8, 48), (3000, 64, 2, 32)])
+def test_group_repeated_ids(dev, t, e, k, tm):
+    """A token that names one expert more than once: every entry is counted and one expert's entries keep ascending
+    i, as p_group's ordered scan gives them (lfm2moe/kernels/mk.mojo:123-161); the lists follow p_expert_lists."""
+    import torch
+    from aq import _lib
+    rng = np.random.default_rng(t + e + k)
+    ids = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+    rep = rng.choice(t, size=max(1, t // 10), replace=False)
+    ids[rep, k - 1] = ids[rep, 0]            # the first and last choice of these tokens coincide
+    ids[0, :] = ids[0, 0]                    # one token names a single expert k times
+    ref = orc.p_group(ids, e, tm)
+    max_rows = _lib.lib().aq_moe_group_max_rows(t, k, e, tm)
+    max_tiles = _lib.lib().aq_moe_group_max_tiles(t, k, e, tm)
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts, offs, slot = torch.empty(e, **i32), torch.empty(e + 1, **i32), torch.empty(t * k, **i32)
+    src, tiles, nt = torch.empty(max_rows, **i32), torch.empty(2 * max_tiles, **i32), torch.empty(1, **i32)
+    torch.ops.aq.moe_group(_i32(ids, dev), e, tm, counts, offs, slot, src, tiles, nt)
+    np.testing.assert_array_equal(to_np(counts), ref["cnt"])
+    assert to_np(counts).sum() == t * k
+    np.testing.assert_array_equal(to_np(offs)[:e], ref["offs"])
+    np.testing.assert_array_equal(to_np(slot), ref["slot"])
+    np.testing.assert_array_equal(to_np(src)[:ref["rows_total"]], ref["src"])
+    n_t = int(to_np(nt)[0])
+    np.testing.assert_array_equal(to_np(tiles)[:2 * n_t].reshape(-1, 2), ref["tiles"])
+    lists_ref, counts_ref = orc.expert_lists(ids, e, t * k)
+    lists, counts2 = torch.full((e, t * k), -1, **i32), torch.empty(e, **i32)
+    scratch = torch.empty(e + 1 + 4 * t * k + 1, **i32)
+    torch.ops.aq.moe_expert_lists(_i32(ids, dev), e, lists, counts2, 8, torch.empty(0, **i32),
+                                  torch.empty(0, **i32), scratch)
+    np.testing.assert_array_equal(to_np(counts2), counts_ref)
+    got = to_np(lists)
+    for ex in range(e):
+        np.testing.assert_array_equal(got[ex, :counts_ref[ex]], lists_ref[ex, :counts_ref[ex]])
 
 
 def test_moe_sum_identity_slots(dev):
