@@ -71,6 +71,17 @@ int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16
  * (its kernels need no scratch). */
 int64_t aq_gemm_q4_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
+/* aq_gemm_q4 without a workspace argument and without any allocation: the split-K partials live in a static device
+ * array of AQ_GEMM_NOALLOC_SCRATCH_BYTES, one per GPU, held until the process ends. Same plan, kernels and result as
+ * aq_gemm_q4 given a large enough workspace (bit for bit). A shape whose partials exceed the array (at most
+ * aq_gemm_q4_workspace_bytes(m, n, k) bytes) is refused with AQ_ERR_CAPACITY; `stream` must belong to the current
+ * device (else AQ_ERR_ARG). Every call on one GPU shares its array, so calls that overlap on one GPU race: order them
+ * on one stream. No counterpart in the reference; it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+#define AQ_GEMM_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int aq_gemm_q4_noalloc(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y, int64_t m,
+                       int64_t n, int64_t k, int32_t group, int32_t add, void* stream);
+
 /* ---- ternary (T2W) GEMM on MFMA, prefill ----------------------------------------------------------------------------
  * Y[m, n] = (add ? Y : 0) + sum_k X[m, k] * (code(k, n) - 1) * s[k/128, n], X fp16 or fp32 (rounded to fp16),
  * T2W w [K/16, N], s fp16 [K/128, N], fp32 accumulation (rel 1e-2 bar). Requires K % 128 == 0.

@@ -23,6 +23,7 @@ SIGNATURES: dict[str, list] = {
     "aq_gate_up_q4": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _p],
     "aq_gemm_q4": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p],
     "aq_gemm_q4_workspace_bytes": [_i64, _i64, _i64],
+    "aq_gemm_q4_noalloc": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p],
     "aq_gemm_t2": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "aq_gemm_t2_workspace_bytes": [_i64, _i64, _i64],
     "aq_moe_gemm_q4": [_p, _i32, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _i32, _i32, _i64, _i32, _p, _p],

@@ -16,6 +16,7 @@
 // 8-chunk), so a fragment is one ds_read_b128 per lane; slots are XOR-swizzled to keep staging writes 2-way. LDS is
 // double-buffered: the next super-step's X and W are fetched into registers while this one is multiplied.
 #include <algorithm>
+#include <mutex>
 
 #include "aq_gemm.h"
 
@@ -413,10 +414,14 @@ static int gemm_dispatch(const void* x, const uint32_t* wq, const uint16_t* ws, 
              : gemm_mb<FMT, G32, XF32, false, false>(x, wq, ws, y, part, M, N, K, group, p, s);
 }
 
+static int noalloc_scratch(hipStream_t s, void** ptr);
+
+// noalloc (aq_gemm_q4_noalloc): the split-K partials go to this file's static scratch array, whose size ws_bytes
+// gives, and a shape whose partials exceed it is refused instead of running in one pass.
 template <int FMT>
 static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_t* ws, float* y, int64_t m,
                       int64_t n, int64_t k, int32_t group, int32_t add, void* workspace, int64_t ws_bytes,
-                      void* stream) {
+                      void* stream, bool noalloc = false) {
   if (!x || !wq || !ws || !y) return AQ_ERR_NULL;
   if (m <= 0 || n <= 0 || k <= 0 || k % (FMT == kT2 ? 128 : 32)) return AQ_ERR_SHAPE;
   if (m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return AQ_ERR_SHAPE;
@@ -431,6 +436,14 @@ static int gemm_entry(const void* x, int xf32, const uint32_t* wq, const uint16_
   const bool g32 = FMT == kT2 || group % 32 == 0;
   if (FMT == kT2) group = 128;
   GemmPlan p = plan_gemm(M, N, K, !xf32 && g32 && x16_shape_ok(K, group));
+  if (noalloc) {
+    workspace = nullptr;
+    if (p.splits > 1) {
+      if (gemm_workspace_bytes(p, M, N) > ws_bytes) return AQ_ERR_CAPACITY;
+      const int st = noalloc_scratch(s, &workspace);
+      if (st != AQ_OK) return st;
+    }
+  }
   if (p.splits > 1 && (!workspace || ws_bytes < gemm_workspace_bytes(p, M, N) || !aligned(workspace, 16))) {
     p.splits = 1;  // no (or too small a) workspace: one pass over K
     p.sup_per_split = (K + kSuper - 1) / kSuper;
@@ -520,6 +533,45 @@ extern "C" int aq_moe_gemm_q4(const void* x, int32_t x_is_f32, int64_t x_rows, c
 
 namespace aq {
 }  // namespace aq
+
+// ---- the allocation-free variant of aq_gemm_q4 ------------------------------------------------------------------
+// Its split-K partials live in `scratch`, one array per GPU (the device code object's copy, held until the process
+// ends); calls on one GPU share it, so calls that overlap there race. Host code never passes the array's name (a
+// host-side stand-in, not a device address) to a kernel: the device address comes from hipGetSymbolAddress, once per
+// device with that device current, and is kept per device.
+static __device__ __align__(256) uint8_t scratch[AQ_GEMM_NOALLOC_SCRATCH_BYTES];
+
+namespace aq {
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int noalloc_scratch(hipStream_t s, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return AQ_ERR_LAUNCH;
+  if (s) {  // the stream's device must be the current one: the symbol is looked up on the current device
+    int sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess) return AQ_ERR_LAUNCH;
+    if (sdev != dev) return AQ_ERR_ARG;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return AQ_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return AQ_OK;
+}
+
+}  // namespace aq
+
+extern "C" int aq_gemm_q4_noalloc(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y,
+                                  int64_t m, int64_t n, int64_t k, int32_t group, int32_t add, void* stream) {
+  return aq::gemm_entry<aq::kQ4>(x, x_is_f32, wq, ws, y, m, n, k, group, add, nullptr, AQ_GEMM_NOALLOC_SCRATCH_BYTES,
+                                 stream, true);
+}
 
 extern "C" int aq_gemm_q4(const void* x, int32_t x_is_f32, const uint32_t* wq, const uint16_t* ws, float* y,
                           int64_t m, int64_t n, int64_t k, int32_t group, int32_t add, void* workspace,

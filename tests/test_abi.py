@@ -243,3 +243,16 @@ def test_moe_combine_and_gemm_validate_shapes_before_launch():
     _raises(gm(), "device")
     _raises(gm(ws=torch.zeros((64, 1), dtype=torch.float16)), "ws must be")
     _raises(gm(out=torch.zeros((48, 31))), "out must be")
+
+
+def test_gemm_noalloc_refuses_partials_beyond_its_array():
+    """aq_gemm_q4_noalloc keeps split-K partials in a static 32 MiB array per GPU: a shape needing more is refused with
+    AQ_ERR_CAPACITY before any device call."""
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    assert lib.aq_gemm_q4_workspace_bytes(1120, 4096, 8192) > (32 << 20)
+    assert lib.aq_gemm_q4_noalloc(p, 0, p, p, p, 1120, 4096, 8192, 32, 0, None) == 6
+    assert lib.aq_gemm_q4_noalloc(p, 0, p, p, p, 431, 2048, 8016, 32, 0, None) == 1   # K % 32
+    assert lib.aq_gemm_q4_noalloc(p + 4, 0, p, p, p, 431, 2048, 8192, 32, 0, None) == 3
