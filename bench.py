@@ -1,7 +1,7 @@
 """Benchmark of the weight-quantized matmul path on one MI355X; prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-    python bench.py --profile dominant|copy|decode|heads   # short runs for rocprofv3 passes
+    python bench.py --profile dominant|copy|decode|heads|moe   # short runs for rocprofv3 passes
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
   value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
@@ -30,6 +30,7 @@ import sys
 import time
 from pathlib import Path
 
+T_START = time.perf_counter()
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "mojo-adreno_amd"))
 
@@ -218,6 +219,8 @@ def profile_run(dev, what: str):
         bench_decode_c4(dev, replays=20)
     elif what == "heads":  # the three output heads with their argmax
         bench_heads(dev)
+    elif what == "moe":  # C3: the block at 404 tokens and one token at a time
+        bench_moe_c3(dev)
     else:
         nbytes = 256 << 20
         a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -321,13 +324,17 @@ def bench_moe_c3(dev):
     logits = _dev(d["logits"], dev)
     out = torch.empty((404, 2048), dtype=torch.float32, device=dev)
     t404 = GraphTimer([lambda b=b: b.forward(x, logits, out) for b in sets]).time(replays=5) / 2
-    x1, l1 = x[0].contiguous(), logits[0].contiguous()
+    # one token at a time: 16 different tokens (so different experts, whose rows come from HBM rather than the
+    # Infinity Cache) over both weight sets
+    toks = [(x[i].contiguous(), logits[i].contiguous()) for i in range(16)]
     o1 = torch.empty(2048, dtype=torch.float32, device=dev)
-    t1 = GraphTimer([lambda b=b: b.decode(x1, l1, o1) for b in sets]).time(replays=20) / 2
+    calls = [(lambda b=b, xt=xt, lt=lt: b.decode(xt, lt, o1)) for xt, lt in toks for b in sets]
+    t1 = GraphTimer(calls).time(replays=10) / len(calls)
     wbytes = 128 * (1536 * 2048 + 2048 * 768) * 0.5625
     return dict(ms_404=round(t404 * 1e3, 4), ms_1=round(t1 * 1e3, 4),
                 gbs_404_weights=round(wbytes / t404 / 1e9, 1),
-                gbs_1_active=round(8 * (1536 * 2048 + 2048 * 768) * 0.5625 / t1 / 1e9, 1))
+                gbs_1_active=round(8 * (1536 * 2048 + 2048 * 768) * 0.5625 / t1 / 1e9, 1),
+                tokens_1_rotation=len(toks))
 
 
 def bench_decode_c4(dev, replays: int = 40):
@@ -492,9 +499,9 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("dominant", "copy", "decode", "heads"),
-                    help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, C4 decode steps or "
-                         "the output heads")
+    ap.add_argument("--profile", choices=("dominant", "copy", "decode", "heads", "moe"),
+                    help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, C4 decode steps, "
+                         "the output heads or the C3 MoE block")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every kernel runs on one GPU's share)",
@@ -509,15 +516,22 @@ def main():
         profile_run(dev, args.profile)
         return
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    c1 = bench_gemm_c1(dev, args.steps, args.warmup)
-    wall = time.perf_counter() - t0
-    r = bench_gemv_c0(dev, 128, 10)
-    c2 = bench_ternary_c2(dev)
-    c3 = bench_moe_c3(dev)
-    c4 = bench_decode_c4(dev)
-    heads = bench_heads(dev)
-    dom = time_dominant(dev)
+    legs = {}  # wall-clock seconds of each leg (setup, warmup, timing and checks included)
+
+    def leg(name, fn, *a):
+        t = time.perf_counter()
+        res = fn(*a)
+        torch.cuda.synchronize()
+        legs[name] = round(time.perf_counter() - t, 2)
+        return res
+
+    c1 = leg("c1", bench_gemm_c1, dev, args.steps, args.warmup)
+    r = leg("c0", bench_gemv_c0, dev, 128, 10)
+    c2 = leg("c2", bench_ternary_c2, dev)
+    c3 = leg("c3", bench_moe_c3, dev)
+    c4 = leg("c4", bench_decode_c4, dev)
+    heads = leg("heads", bench_heads, dev)
+    dom = leg("roofline", time_dominant, dev)
     value = c1["flop"] / c1["t_step"] / 1e12
     achieved = dom["flop"] / dom["t"] / 1e12
     gemv = r["bytes"] / r["t_burst"] / 1e9
@@ -542,14 +556,15 @@ def main():
         "moe_c3": c3,
         "decode_c4": c4,
         "heads": heads,
-        "wall_s": round(wall, 2),
     }
     if not args.skip_cpu:
-        out["cpu_baseline"] = cpu_baseline_gemm()
-        out["gemv_c0"]["cpu_baseline"] = cpu_baseline_gemv()
-        out["decode_c4"]["cpu_baseline"] = cpu_baseline_decode()
-        out["ternary_c2"]["cpu_baseline"] = cpu_baseline_ternary()
-        out["moe_c3"]["cpu_baseline"] = cpu_baseline_moe()
+        out["cpu_baseline"] = leg("cpu_c1", cpu_baseline_gemm)
+        out["gemv_c0"]["cpu_baseline"] = leg("cpu_c0", cpu_baseline_gemv)
+        out["decode_c4"]["cpu_baseline"] = leg("cpu_c4", cpu_baseline_decode)
+        out["ternary_c2"]["cpu_baseline"] = leg("cpu_c2", cpu_baseline_ternary)
+        out["moe_c3"]["cpu_baseline"] = leg("cpu_c3", cpu_baseline_moe)
+    out["legs_s"] = legs
+    out["wall_s"] = round(time.perf_counter() - T_START, 2)  # the whole run, from the first import
     print(json.dumps(out), flush=True)
 
 

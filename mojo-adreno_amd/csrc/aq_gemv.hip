@@ -10,6 +10,7 @@
 // decoded word to all T tokens. A word is decoded as q + 8 (XOR 0x88888888, byte masks -> v_cvt_f32_ubyte), and
 // 8 * sum(x) is subtracted once per chunk: two VALU ops per weight. Row sums end in a wave reduction.
 #include "aq_common.h"
+#include "aq_moe_decode.h"
 
 namespace aq {
 
@@ -707,7 +708,13 @@ extern "C" int aq_moe_down_q4(const uint32_t* wq, const uint16_t* ws, int64_t ex
   if (!ids || !weights) return AQ_ERR_NULL;
   if (topk <= 0 || topk > 8 || d <= 0 || experts <= 0 || experts * d > INT32_MAX) return AQ_ERR_SHAPE;
   if (f > 0 && experts * d * (f / 2) >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;  // stacked W below 2 GiB
-  // the expert slots are the kernel's "tokens": act [topk, f] holds one activation vector per slot
+  if (aq::moe_down_dec_ok(f, group, topk) && f % group == 0) {  // one wave per expert slot, 8 lanes a row
+    if (!wq || !ws || !act || !y) return AQ_ERR_NULL;
+    if (!aq::aligned(wq, 16) || !aq::aligned(act, 16)) return AQ_ERR_ALIGN;
+    return aq::launch_moe_down_dec(wq, ws, ids, weights, act, y, d, f, group, (int32_t)experts, topk, add,
+                                   reinterpret_cast<hipStream_t>(stream));
+  }
+  // other groups and wider f: the expert slots are the GEMV's "tokens", act [topk, f] one activation vector per slot
   const aq::MoeArgs moe{ids, weights, (int)experts, add ? 1 : 0};
   return aq::gemv_entry<aq::kMoeDown>(wq, ws, act, y, d, f, group, 0, topk, moe, stream);
 }
