@@ -317,7 +317,7 @@ def bench_moe_c3(dev):
             w = [torch.randint(-2 ** 31, 2 ** 31 - 1, t.shape, dtype=torch.int32, device=dev, generator=gen)
                  if t.dtype == torch.int32 else (torch.rand(t.shape, device=dev, generator=gen) * 0.03 + 1e-3).half()
                  for t in sets[0]._w]
-        blk = moe.MoeBlock(*w, 128, 2048, 768, 32, 8, max_tokens=404, tm=48)
+        blk = moe.MoeBlock(*w, 128, 2048, 768, 32, 8, max_tokens=404, tm=32)
         blk._w = w
         sets.append(blk)
     x = _dev(d["x"], dev)

@@ -19,7 +19,7 @@ class MoeBlock:
     ``[E * 2F, D/8]`` (expert e's gate rows at e*2F, up rows at e*2F + F) and down Q4W ``[E * D, F/8]``."""
 
     def __init__(self, gu_q, gu_s, dn_q, dn_s, experts: int, hidden: int, ffn: int, group: int, topk: int = 8,
-                 max_tokens: int = 512, tm: int = 48):
+                 max_tokens: int = 512, tm: int = 32):
         self.gu_q, self.gu_s, self.dn_q, self.dn_s = gu_q, gu_s, dn_q, dn_s
         self.E, self.D, self.F, self.G, self.K, self.tm = experts, hidden, ffn, group, topk, tm
         dev = gu_q.device
