@@ -1,7 +1,7 @@
 """Benchmark of the weight-quantized matmul path on one MI355X; prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-    python bench.py --profile dominant|copy|decode|heads|moe   # short runs for rocprofv3 passes
+    python bench.py --profile dominant|copy|decode|heads|gemvs|moe   # short runs for rocprofv3 passes
 
 Workload (BASELINE.json metric "int4 GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s; MoE layer ms"):
   value     C1 int4 prefill GEMM TFLOP/s: one step = one Llama-3.2-1B layer's projections at M = 431 fp16 tokens
@@ -82,6 +82,35 @@ class GraphTimer:
         return start.elapsed_time(end) / 1e3 / replays
 
 
+class ReadCeiling:
+    """The streaming-read ceiling of a matrix-vector launch: aq_stream_read over the same number of bytes (every 16
+    bytes loaded once with the weights' streaming cache policy, nothing decoded), timed like the GEMVs (a graph burst
+    over distinct slices of a pool larger than the 256 MB Infinity Cache), the best of several workgroup counts."""
+
+    BLOCKS = (0, 512, 1024, 2048, 4096)
+
+    def __init__(self, dev, pool_mb: int = 640):
+        import torch
+        self.pool = torch.empty(pool_mb << 18, dtype=torch.int32, device=dev)  # contents are not read for meaning
+        self.sink = torch.empty(8192, dtype=torch.int32, device=dev)
+        self.cache = {}
+
+    def us(self, nbytes: int) -> float:
+        import torch
+        n = -(-nbytes // 16) * 16
+        if n in self.cache:
+            return self.cache[n]
+        stride = -(-n // 4096) * 4096  # distinct 4 KB-aligned slices
+        copies = max(2, min(256, self.pool.numel() * 4 // stride))
+        best = float("inf")
+        for blocks in self.BLOCKS:
+            launches = [(lambda i=i: torch.ops.aq.stream_read(self.pool[i * stride // 4:(i * stride + n) // 4],
+                                                              self.sink, blocks)) for i in range(copies)]
+            best = min(best, GraphTimer(launches).time(replays=3) / copies)
+        self.cache[n] = round(best * 1e6, 3)
+        return self.cache[n]
+
+
 def bench_gemv_c0(dev, steps: int, warmup: int, pool_mb: int = 600):
     """C0 int4 GEMV: burst (graph of distinct-copy launches) and single cold launch."""
     import numpy as np
@@ -124,7 +153,7 @@ def bench_gemv_c0(dev, steps: int, warmup: int, pool_mb: int = 600):
         cold.append(a.elapsed_time(b) / 1e3)
     s.synchronize()
     t_cold = float(np.median(cold))
-    return dict(bytes=per, flop=2 * n * k, t_step=t_step, t_burst=t_burst, t_cold=t_cold, pool_copies=copies,
+    return dict(bytes=per, wbytes=n * k // 2 + n * (k // g) * 2, flop=2 * n * k, t_step=t_step, t_burst=t_burst, t_cold=t_cold, pool_copies=copies,
                 pool_mb=round(copies * per / 1e6, 1), steps=len(seq))
 
 
@@ -217,8 +246,10 @@ def profile_run(dev, what: str):
             fn()
     elif what == "decode":  # C4: 20 graph-replayed decode steps at context 512
         bench_decode_c4(dev, replays=20)
-    elif what == "heads":  # the three output heads with their argmax
-        bench_heads(dev)
+    elif what == "heads":  # the three output heads with their argmax (and their streaming-read ceilings)
+        bench_heads(dev, ReadCeiling(dev))
+    elif what == "gemvs":  # the C4 step's GEMVs one at a time (and their streaming-read ceilings)
+        bench_gemv_c4(dev, ReadCeiling(dev))
     elif what == "moe":  # C3: the block at 404 tokens and one token at a time
         bench_moe_c3(dev)
     else:
@@ -363,11 +394,64 @@ def bench_decode_c4(dev, replays: int = 40):
     return out
 
 
+def bench_gemv_c4(dev, ceil: ReadCeiling, pool_mb: int = 600):
+    """The C4 decode step's int4 GEMVs one at a time, each launched as the step launches it: q|k|v with the attention
+    RMSNorm fused into its x staging, o combining the split-attention states while staging, gate|up with the MLP
+    RMSNorm and the SwiGLU product fused, down adding into the residual, and the lm_head with the final RMSNorm and
+    the device argmax (two launches). Microseconds per launch by graph burst over a rotating pool of distinct weight
+    copies (more than the Infinity Cache holds), beside ReadCeiling's time for the same weight and scale bytes."""
+    import torch
+    from aq import ops
+    from aq.llama import LlamaConfig
+    cfg = LlamaConfig()
+    d, f, g = cfg.dim, cfg.ffn, cfg.group
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(106)
+    x = torch.randn(d, device=dev, generator=gen)
+    xf = torch.randn(f, device=dev, generator=gen)
+    norm = (torch.rand(d, device=dev, generator=gen) + 0.5).half()
+    splits = max(1, min(ops.ATTN_MAX_SPLITS, cfg.max_pos // 64))
+    parts = torch.randn(ops.attn_parts_numel(cfg.heads, splits), device=dev, generator=gen)
+    ml = parts[cfg.heads * splits * 64:].view(-1, 2)
+    ml[:, 0] = 0.0
+    ml[:, 1] = 1.0
+    qkv = torch.empty(cfg.qkv, dtype=torch.float32, device=dev)
+    act = torch.empty(f, dtype=torch.float32, device=dev)
+    res = torch.zeros(d, dtype=torch.float32, device=dev)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
+    cand = torch.zeros(ops.HEAD_CANDIDATES, dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.empty(0, dtype=torch.int32, device=dev)
+    a = torch.ops.aq
+    shapes = {  # name: (rows, K, launch)
+        "qkv": (cfg.qkv, d, lambda m: a.rmsnorm_gemv_q4(m[0], m[1], x, norm, cfg.eps, qkv, g)),
+        "o": (d, cfg.heads * cfg.head_dim, lambda m: a.attn_out_q4(m[0], m[1], parts, splits, res, g)),
+        "gate_up": (2 * f, d, lambda m: a.rmsnorm_gate_up_q4(m[0], m[1], x, norm, cfg.eps, act, g)),
+        "down": (d, f, lambda m: a.gemv_q4(m[0], m[1], xf, res, g, True)),
+        "lm_head": (cfg.vocab, d, lambda m: a.head_argmax_q4(m[0], m[1], x, norm, cfg.eps, logits, g, cand, tok, pos,
+                                                             hist, 0)),
+    }
+    out = {}
+    for name, (rows, k, launch) in shapes.items():
+        wbytes = rows * k // 2 + rows * (k // g) * 2
+        copies = max(2, int(pool_mb * 1e6 // wbytes))
+        mats = [(torch.randint(-2 ** 31, 2 ** 31 - 1, (rows, k // 8), dtype=torch.int32, device=dev, generator=gen),
+                 (torch.rand((rows, k // g), device=dev, generator=gen) * 0.03 + 1e-3).half()) for _ in range(copies)]
+        t = GraphTimer([lambda m=m: launch(m) for m in mats]).time(replays=5) / copies
+        del mats
+        torch.cuda.empty_cache()
+        read = ceil.us(wbytes)
+        out[name] = dict(us=round(t * 1e6, 3), read_us=read, frac_of_read=round(read / (t * 1e6), 3),
+                         gbs=round(wbytes / t / 1e9, 1), mb=round(wbytes / 1e6, 2), pool_copies=copies)
+    return out
+
+
 def _q6_bytes(rows, cols):
     return rows * (cols // 256) * 210 + cols * 4 + rows * 4
 
 
-def bench_heads(dev, pool_mb: int = 640):
+def bench_heads(dev, ceil: ReadCeiling, pool_mb: int = 640):
     """Output heads with their device argmax (head GEMV + argmax step, two launches): LFM2.5's Q6_K tied head
     (128000 x 2048), Bonsai's ternary head (248320 x 2048, X2H input) and Llama-3.2-1B's int4 lm_head (128256 x 2048,
     G = 32), each over a rotating pool of distinct weight copies larger than the 256 MB Infinity Cache. Bytes a
@@ -388,8 +472,9 @@ def bench_heads(dev, pool_mb: int = 640):
         copies = max(2, int(pool_mb * 1e6 // per))
         mats = [make() for _ in range(copies)]
         t = GraphTimer([lambda m=m: launch(m) for m in mats]).time(replays=5) / copies
+        read = ceil.us(per)
         out[name] = dict(us=round(t * 1e6, 2), gbs=round(per / t / 1e9, 1), frac_hbm=round(per / t / 1e9 / HBM_PEAK_GBS, 4),
-                         mb=round(per / 1e6, 1), pool_copies=copies)
+                         mb=round(per / 1e6, 1), pool_copies=copies, read_us=read, frac_of_read=round(read / (t * 1e6), 3))
         del mats
         torch.cuda.empty_cache()
 
@@ -499,9 +584,9 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("dominant", "copy", "decode", "heads", "moe"),
+    ap.add_argument("--profile", choices=("dominant", "copy", "decode", "heads", "gemvs", "moe"),
                     help="short run for a rocprofv3 pass: the dominant kernel, a calibration copy, C4 decode steps, "
-                         "the output heads or the C3 MoE block")
+                         "the output heads, the C4 step's GEMVs one at a time or the C3 MoE block")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every kernel runs on one GPU's share)",
@@ -530,7 +615,10 @@ def main():
     c2 = leg("c2", bench_ternary_c2, dev)
     c3 = leg("c3", bench_moe_c3, dev)
     c4 = leg("c4", bench_decode_c4, dev)
-    heads = leg("heads", bench_heads, dev)
+    ceil = ReadCeiling(dev)
+    c4["gemvs"] = leg("c4_gemvs", bench_gemv_c4, dev, ceil)
+    heads = leg("heads", bench_heads, dev, ceil)
+    c0_read = ceil.us(r["wbytes"])
     dom = leg("roofline", time_dominant, dev)
     value = c1["flop"] / c1["t_step"] / 1e12
     achieved = dom["flop"] / dom["t"] / 1e12
@@ -551,7 +639,8 @@ def main():
         "gemv_c0": {"gbs_graph_burst": round(gemv, 2), "frac_hbm": round(gemv / HBM_PEAK_GBS, 4),
                     "gbs_single_cold": round(r["bytes"] / r["t_cold"] / 1e9, 2),
                     "us_burst": round(r["t_burst"] * 1e6, 3), "us_single_cold": round(r["t_cold"] * 1e6, 3),
-                    "pool_mb": r["pool_mb"]},
+                    "pool_mb": r["pool_mb"], "read_us_graph_burst": c0_read,
+                    "frac_of_read": round(c0_read / (r["t_burst"] * 1e6), 3)},
         "ternary_c2": c2,
         "moe_c3": c3,
         "decode_c4": c4,

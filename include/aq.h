@@ -291,6 +291,15 @@ int64_t aq_head_q6_candidates(int64_t rows, int64_t cols);
 int aq_embed_q6(const uint8_t* q, const uint16_t* d, int64_t rows, int64_t cols, const int32_t* ids, int32_t ntok,
                 float* x, void* stream);
 
+/* ---- measurement ---------------------------------------------------------------------------------------------------
+ * Streaming read: sink[b] = the XOR of the 32-bit words that workgroup b of `blocks` (0: one vector-load pass a thread,
+ * at most 1024) reads, every 16 bytes of p [bytes] read once with the matrix-vector kernels' streaming cache policy,
+ * nothing else computed; the XOR of sink[0 .. blocks) is the XOR of the whole buffer. bytes % 16 == 0, bytes < 2^31,
+ * blocks <= AQ_STREAM_READ_MAX_BLOCKS, sink holds the launch's workgroup count of words. No counterpart in the
+ * reference: a launch over a weight matrix's bytes is the ceiling its matrix-vector product is measured against. */
+#define AQ_STREAM_READ_MAX_BLOCKS 8192
+int aq_stream_read(const void* p, int64_t bytes, int32_t blocks, uint32_t* sink, void* stream);
+
 /* ---- weight-format converters (host code: host pointers, synchronous, no GPU) ----------------------------------
  * They write the layouts above from the reference's source formats, byte for byte as the reference's converters do. */
 

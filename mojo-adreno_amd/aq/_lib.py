@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "aq_head_argmax_q6": [_p, _p, _p, _p, ctypes.c_float, _p, _i64, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _p],
     "aq_head_q6_candidates": [_i64, _i64],
     "aq_embed_q6": [_p, _p, _i64, _i64, _p, _i32, _p, _p],
+    "aq_stream_read": [_p, _i64, _i32, _p, _p],
     "aq_t2_packed_linear": [_p, _p, _p, _p, _i64, _i64, _p],
     "aq_t2_packed_reduce": [_p, _p, _i64, _i32, _p],
     "aq_pack_half": [_p, _p, _i64, _p],

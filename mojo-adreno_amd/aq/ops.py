@@ -657,3 +657,24 @@ for _name, _fn in (("rmsnorm_gemv_q4", _rmsnorm_gemv_q4_impl), ("rmsnorm_gate_up
                    ("attn_decode_split", _attn_decode_split_impl), ("attn_out_q4", _attn_out_q4_impl),
                    ("head_argmax_q4", _head_argmax_q4_impl)):
     _LIB.impl(_name, _fn, "CUDA")
+
+
+# ---- measurement ---------------------------------------------------------------------------------------------------
+
+STREAM_READ_MAX_BLOCKS = 8192
+_LIB.define("stream_read(Tensor p, Tensor(a!) sink, int blocks) -> ()")
+
+
+def _stream_read_impl(p, sink, blocks):
+    """sink[b] = XOR of the 32-bit words workgroup b reads; every byte of p read once (the streaming-read ceiling)."""
+    _dev(p, sink)
+    nbytes = p.numel() * p.element_size()
+    _check(nbytes % 16 == 0, "p must hold a multiple of 16 bytes")
+    _check(0 <= blocks <= STREAM_READ_MAX_BLOCKS, f"blocks must be in 0..{STREAM_READ_MAX_BLOCKS}")
+    _check(sink.dtype in (torch.int32, torch.uint32), "sink must be int32/uint32 words")
+    need = blocks if blocks else min(1024, -(-(nbytes // 16) // 1024))
+    _check(sink.numel() >= need, f"sink must hold {need} words")
+    _lib.call("aq_stream_read", _ptr(p), nbytes, blocks, _ptr(sink), _stream(p))
+
+
+_LIB.impl("stream_read", _stream_read_impl, "CUDA")

@@ -256,3 +256,16 @@ def test_gemm_noalloc_refuses_partials_beyond_its_array():
     assert lib.aq_gemm_q4_noalloc(p, 0, p, p, p, 1120, 4096, 8192, 32, 0, None) == 6
     assert lib.aq_gemm_q4_noalloc(p, 0, p, p, p, 431, 2048, 8016, 32, 0, None) == 1   # K % 32
     assert lib.aq_gemm_q4_noalloc(p + 4, 0, p, p, p, 431, 2048, 8192, 32, 0, None) == 3
+
+
+def test_stream_read_rejects_bad_arguments_before_launch():
+    import aq
+    lib = aq.lib()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
+    assert lib.aq_stream_read(None, 4096, 0, p, None) == 5
+    assert lib.aq_stream_read(p, 4100, 0, p, None) == 1          # not whole 16-byte vectors
+    assert lib.aq_stream_read(p, 0, 0, p, None) == 1
+    assert lib.aq_stream_read(p, 1 << 31, 0, p, None) == 6      # 32-bit offsets
+    assert lib.aq_stream_read(p, 4096, 8193, p, None) == 7      # beyond AQ_STREAM_READ_MAX_BLOCKS
+    assert lib.aq_stream_read(p + 4, 4096, 0, p, None) == 3
