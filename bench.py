@@ -87,12 +87,13 @@ class ReadCeiling:
     bytes loaded once with the weights' streaming cache policy, nothing decoded), timed like the GEMVs (a graph burst
     over distinct slices of a pool larger than the 256 MB Infinity Cache), the best of several workgroup counts."""
 
-    BLOCKS = (0, 512, 1024, 2048, 4096)
+    BLOCKS = (0, 1024, 2048, 4096)
 
     def __init__(self, dev, pool_mb: int = 640):
         import torch
+        from aq import ops  # noqa: F401  (registers torch.ops.aq)
         self.pool = torch.empty(pool_mb << 18, dtype=torch.int32, device=dev)  # contents are not read for meaning
-        self.sink = torch.empty(8192, dtype=torch.int32, device=dev)
+        self.sink = torch.empty(4 * 8192, dtype=torch.int32, device=dev)
         self.cache = {}
 
     def us(self, nbytes: int) -> float:
@@ -394,7 +395,7 @@ def bench_decode_c4(dev, replays: int = 40):
     return out
 
 
-def bench_gemv_c4(dev, ceil: ReadCeiling, pool_mb: int = 600):
+def bench_gemv_c4(dev, ceil: ReadCeiling, pool_mb: int = 600, names=None):
     """The C4 decode step's int4 GEMVs one at a time, each launched as the step launches it: q|k|v with the attention
     RMSNorm fused into its x staging, o combining the split-attention states while staging, gate|up with the MLP
     RMSNorm and the SwiGLU product fused, down adding into the residual, and the lm_head with the final RMSNorm and
@@ -434,6 +435,8 @@ def bench_gemv_c4(dev, ceil: ReadCeiling, pool_mb: int = 600):
     }
     out = {}
     for name, (rows, k, launch) in shapes.items():
+        if names and name not in names:
+            continue
         wbytes = rows * k // 2 + rows * (k // g) * 2
         copies = max(2, int(pool_mb * 1e6 // wbytes))
         mats = [(torch.randint(-2 ** 31, 2 ** 31 - 1, (rows, k // 8), dtype=torch.int32, device=dev, generator=gen),

@@ -292,11 +292,12 @@ int aq_embed_q6(const uint8_t* q, const uint16_t* d, int64_t rows, int64_t cols,
                 float* x, void* stream);
 
 /* ---- measurement ---------------------------------------------------------------------------------------------------
- * Streaming read: sink[b] = the XOR of the 32-bit words that workgroup b of `blocks` (0: one vector-load pass a thread,
- * at most 1024) reads, every 16 bytes of p [bytes] read once with the matrix-vector kernels' streaming cache policy,
- * nothing else computed; the XOR of sink[0 .. blocks) is the XOR of the whole buffer. bytes % 16 == 0, bytes < 2^31,
- * blocks <= AQ_STREAM_READ_MAX_BLOCKS, sink holds the launch's workgroup count of words. No counterpart in the
- * reference: a launch over a weight matrix's bytes is the ceiling its matrix-vector product is measured against. */
+ * Streaming read: every 16 bytes of p [bytes] read once with the matrix-vector kernels' streaming cache policy,
+ * nothing else computed, by `blocks` workgroups of 4 waves (0: one 8 KB page each, at most
+ * AQ_STREAM_READ_MAX_BLOCKS); wave w of workgroup b writes the XOR of the 32-bit words it read to sink[4 b + w], so
+ * the XOR of sink[0 .. 4 blocks) is the XOR of the whole buffer. bytes % 16 == 0, bytes < 2^31,
+ * blocks <= AQ_STREAM_READ_MAX_BLOCKS. No counterpart in the reference: a launch over a weight matrix's bytes is the
+ * ceiling its matrix-vector product is measured against. */
 #define AQ_STREAM_READ_MAX_BLOCKS 8192
 int aq_stream_read(const void* p, int64_t bytes, int32_t blocks, uint32_t* sink, void* stream);
 

@@ -666,13 +666,14 @@ _LIB.define("stream_read(Tensor p, Tensor(a!) sink, int blocks) -> ()")
 
 
 def _stream_read_impl(p, sink, blocks):
-    """sink[b] = XOR of the 32-bit words workgroup b reads; every byte of p read once (the streaming-read ceiling)."""
+    """sink[4 b + w] = XOR of the 32-bit words wave w of workgroup b reads; every byte of p read once (the
+    streaming-read ceiling)."""
     _dev(p, sink)
     nbytes = p.numel() * p.element_size()
     _check(nbytes % 16 == 0, "p must hold a multiple of 16 bytes")
     _check(0 <= blocks <= STREAM_READ_MAX_BLOCKS, f"blocks must be in 0..{STREAM_READ_MAX_BLOCKS}")
     _check(sink.dtype in (torch.int32, torch.uint32), "sink must be int32/uint32 words")
-    need = blocks if blocks else min(1024, -(-(nbytes // 16) // 1024))
+    need = 4 * (blocks if blocks else min(STREAM_READ_MAX_BLOCKS, -(-(nbytes // 16) // 512)))
     _check(sink.numel() >= need, f"sink must hold {need} words")
     _lib.call("aq_stream_read", _ptr(p), nbytes, blocks, _ptr(sink), _stream(p))
 

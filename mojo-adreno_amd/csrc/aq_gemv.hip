@@ -16,6 +16,92 @@ namespace aq {
 
 enum { kStore = 0, kAdd = 1, kGateUp = 2, kMoeGateUp = 3, kMoeDown = 4 };
 
+// x staging of the power-of-two-group products (G >= 32), for word j (x[32c + 8j .. + 7]) of chunk c of token t,
+// a = its first four values, b = the last four. LDS layout (conflict-free for the chunk loop, where lane c reads
+// consecutive 16-byte slots):
+//   xh[t][j][c]   uint4: x[t, 32c + 8j + (0, 4)], (1, 5), (2, 6), (3, 7) as fp16 pairs (the high parts) (T * 4 planes)
+//   xl[t][j][c]   uint4: the same pairs of x - high part (the low parts)                             (T * 4 planes)
+//   xb[t][c]      float4: (bias, 1 / f, -, -): f = the chunk's power-of-two scale (x is staged as f * x, its
+//                 largest magnitude in [2^9, 2^10), so the low parts stay normal fp16, which v_dot2 needs) and
+//                 bias = sum over the chunk of 1032 f x_k (k % 8 even) or 72 f x_k (odd), the magic values' offset
+// The 4 threads of an aligned quad hold the 4 words of one chunk (they exchange maxima and sums by DPP), so whole
+// quads must call it together.
+__device__ __forceinline__ void stage_half(int t, int c, int j, float4 a, float4 b, uint4* __restrict__ xh,
+                                           uint4* __restrict__ xl, float4* __restrict__ xb, int nch) {
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t e = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
+  e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
+  e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
+  const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
+  const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] *= f;
+  uint32_t hw[4], lw[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
+    const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
+    hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+  }
+  xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
+  bias += dpp<0xB1>(0.f, bias);
+  bias += dpp<0x4E>(0.f, bias);
+  if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
+}
+
+// One 32-weight chunk c of R rows (w: their 16 bytes, sc: their fp16 scale bits) against T tokens staged by
+// stage_half: acc[r][t] += scale_r * sum over the chunk of q * x. Each word's 8 codes become 4 fp16 pairs holding
+// the exact values 1024 + n (bits 0-3, 16-19 of the word, and of the word >> 8) or 64 + n (bits 4-7, 20-23),
+// n = stored nibble ^ 8 = q + 8, one v_bitop3 each: ((w ^ 0x8..8) & mask) | magic. Their dot products with the fp16
+// high and low parts of x (v_dot2_f32_f16: exact products, fp32 sums) minus the staged bias sum_k (1032 or 72) x_k
+// leave sum_k q_k x_k.
+template <int R, int T>
+__device__ __forceinline__ void chunk_dot(const uint4* __restrict__ xh, const uint4* __restrict__ xl,
+                                          const float4* __restrict__ xb, int nch, int c, const uint4 (&w)[R],
+                                          const uint16_t (&sc)[R], float (&acc)[R][T]) {
+  half2v pr[R][4][4];  // [row][word][pair]
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
+      const uint32_t w8 = wj >> 8;
+      pr[r][j][0] = __builtin_bit_cast(half2v, ((wj ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
+      pr[r][j][1] = __builtin_bit_cast(half2v, ((wj ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
+      pr[r][j][2] = __builtin_bit_cast(half2v, ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
+      pr[r][j][3] = __builtin_bit_cast(half2v, ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
+    }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const float4 bw = xb[t * nch + c];
+    float part[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[r] = -bw.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 hi = xh[(t * 4 + j) * nch + c], lo = xl[(t * 4 + j) * nch + c];
+      const half2v h4[4] = {__builtin_bit_cast(half2v, hi.x), __builtin_bit_cast(half2v, hi.y),
+                            __builtin_bit_cast(half2v, hi.z), __builtin_bit_cast(half2v, hi.w)};
+      const half2v l4[4] = {__builtin_bit_cast(half2v, lo.x), __builtin_bit_cast(half2v, lo.y),
+                            __builtin_bit_cast(half2v, lo.z), __builtin_bit_cast(half2v, lo.w)};
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], h4[q], part[r], false);
+          part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], l4[q], part[r], false);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]) * bw.y, acc[r][t]);
+  }
+}
+
 // MoE decode: kMoeGateUp outputs o = e * f + j use gate|up rows ids[e] * 2f + j (+ f); kMoeDown output o sums, over
 // expert slots t < tokens (in slot order), rw[t] * (row ids[t] * n_out + o) . x[t]. An id outside [0, experts) selects
 // no row (its contribution is zero).
@@ -65,13 +151,8 @@ template <bool G32, int R, int T, int MODE, int D, int XR>
 __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
                                                  int k, int group, int f, int tokens, MoeArgs moe, Fuse fz) {
-  // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots). G32 (not kMoeDown):
-  //   xh[t][j][c]   uint4: x[t, 32c + 8j + (0, 4)], (1, 5), (2, 6), (3, 7) as fp16 pairs (the high parts) (T * 4 planes)
-  //   xl[t][j][c]   uint4: the same pairs of x - high part (the low parts)                             (T * 4 planes)
-  //   xb[t][c]      float4: (bias, 1 / f, -, -): f = the chunk's power-of-two scale (x is staged as f * x, its
-  //                 largest magnitude in [2^9, 2^10), so the low parts stay normal fp16, which v_dot2 needs) and
-  //                 bias = sum over the chunk of 1032 f x_k (k % 8 even) or 72 f x_k (odd), the magic values' offset
-  // otherwise:
+  // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots). G32 (not kMoeDown): the
+  // xh / xl / xb planes of stage_half. Otherwise:
   //   xs4[t][p][c]  float4 p = 2j + h holds x[t, 32c + 8j + 4h .. + 3]  (T * 8 planes of nch float4)
   //   xsum[t][j][c] sum of x[t, 32c + 8j .. + 7]                        (T * 4 planes of nch floats)
   extern __shared__ float4 lds4[];
@@ -100,47 +181,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 
   // scales travel as raw fp16 bits and are converted where used: a conversion next to its load would wait for it
   const int gsh = __builtin_ctz(group);  // G32 groups are powers of two
-  // One chunk: each word's 8 codes become 4 fp16 pairs holding the exact values 1024 + n (bits 0-3, 16-19 of the
-  // word, and of the word >> 8) or 64 + n (bits 4-7, 20-23), n = stored nibble ^ 8 = q + 8, one v_bitop3 each:
-  // ((w ^ 0x8..8) & mask) | magic. Their dot products with the fp16 high and low parts of x (v_dot2_f32_f16: exact
-  // products, fp32 sums) minus the staged bias sum_k (1032 or 72) x_k leave sum_k q_k x_k.
   auto use_chunk = [&](int c, const uint4 (&w)[R], const uint16_t (&sc)[R], float (&acc)[R][T]) {
-    half2v pr[R][4][4];  // [row][word][pair]
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
-        const uint32_t w8 = wj >> 8;
-        pr[r][j][0] = __builtin_bit_cast(half2v, ((wj ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
-        pr[r][j][1] = __builtin_bit_cast(half2v, ((wj ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
-        pr[r][j][2] = __builtin_bit_cast(half2v, ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
-        pr[r][j][3] = __builtin_bit_cast(half2v, ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
-      }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const float4 bw = xb[t * nch + c];
-      float part[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[r] = -bw.x;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 hi = xh[(t * 4 + j) * nch + c], lo = xl[(t * 4 + j) * nch + c];
-        const half2v h4[4] = {__builtin_bit_cast(half2v, hi.x), __builtin_bit_cast(half2v, hi.y),
-                              __builtin_bit_cast(half2v, hi.z), __builtin_bit_cast(half2v, hi.w)};
-        const half2v l4[4] = {__builtin_bit_cast(half2v, lo.x), __builtin_bit_cast(half2v, lo.y),
-                              __builtin_bit_cast(half2v, lo.z), __builtin_bit_cast(half2v, lo.w)};
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], h4[q], part[r], false);
-            part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], l4[q], part[r], false);
-          }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]) * bw.y, acc[r][t]);
-    }
+    chunk_dot<R, T>(xh, xl, xb, nch, c, w, sc, acc);
   };
 
   // The first chunk of this wave's first row block is requested before x is staged, so its latency overlaps the
@@ -219,6 +261,20 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 #pragma unroll
     for (int d = 0; d < D; ++d) issue_next(wd[d], sd[d], sh[d]);
   }
+  // kAdd, one or two tokens: the residual of the wave's first row block, requested now (lane 0 stores) rather than
+  // after its sums, so its latency is hidden behind the weights'
+  constexpr bool kYPre = kDeep && MODE == kAdd && T <= 2;
+  float ypre[kYPre ? RO : 1][T];
+  if constexpr (kYPre) {
+#pragma unroll
+    for (int r = 0; r < RO; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int o = base0 + r;
+        ypre[r][t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            y_rsrc, (lane == 0 && o < n_out && t < tokens) ? ((uint32_t)t * n_out + o) * 4 : kOOB, 0, 0));
+      }
+  }
 
   // Stage x in one pass. With a norm, x * norm_w is staged and sum(x^2) gathered on the way; the row sums are then
   // scaled by 1 / sqrt(mean(x^2) + eps) (a per-token scalar), which is the RMSNorm'd product.
@@ -240,32 +296,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       b.z *= half_bits_to_float(wn.w & 0xFFFF);
       b.w *= half_bits_to_float(wn.w >> 16);
     }
-    if constexpr (kHalfX) {  // pairs (0, 4), (1, 5), (2, 6), (3, 7), split into fp16 high and low parts
-      float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      // the chunk's scale: the 4 threads of a quad hold its 4 words (whole quads run each iteration: K % 32 == 0)
-      uint32_t e = 0;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
-      e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
-      e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
-      const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
-      const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] *= f;
-      uint32_t hw[4], lw[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
-        const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
-        hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-      }
-      xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
-      bias += dpp<0xB1>(0.f, bias);
-      bias += dpp<0x4E>(0.f, bias);
-      if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
+    if constexpr (kHalfX) {
+      stage_half(t, c, j, a, b, xh, xl, xb, nch);
     } else {
       xs4[(t * 8 + 2 * j) * nch + c] = a;
       xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
@@ -369,7 +401,11 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
         const uint32_t off = (lane == 0 && o < n_out && t < tokens) ? ((uint32_t)t * n_out + o) * 4 : kOOB;
         float v = acc[r][t];
         if constexpr (MODE == kGateUp || MODE == kMoeGateUp) v = silu(v) * acc[RO + r][t];
-        if constexpr (MODE == kAdd) v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+        if constexpr (kYPre) {
+          v += base == base0 ? ypre[r][t] : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+        } else if constexpr (MODE == kAdd) {
+          v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(y_rsrc, off, 0, 0));
+        }
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rsrc, off, 0, 0);
       }
       if constexpr (MODE == kStore) {  // rows arrive in ascending order, so `>` keeps the first maximum; NaN rows
@@ -536,6 +572,130 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   }
 }
 
+// Long-K products with few rows (one token, power-of-two groups >= 32, no fusions; the decode down projection):
+// KS waves share each pair of rows, each taking 1/KS of K, so N = 2048 outputs over K = 8192 run 16 waves per CU
+// instead of 4 (one workgroup of 256 KS threads per 8 outputs; a plain read of the same bytes by 256 workgroups of
+// 256 threads takes 4.1 us against 3.6 us by 1024). The workgroup stages x once (stage_half); each wave requests
+// its two rows' chunks of its K slice first, then its words of x, and the KS partial sums of an output meet in LDS,
+// added in slice order.
+constexpr int kKsRows = 8;  // outputs a workgroup: 4 row pairs
+
+template <int KS, int CPS, int MODE>
+__global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restrict__ wq,
+                                                         const uint16_t* __restrict__ ws,
+                                                         const float* __restrict__ x, float* __restrict__ y,
+                                                         int n_out, int k, int gsh) {
+  extern __shared__ float4 lds4[];
+  __shared__ float red[KS][kKsRows];
+  const int kw = k >> 3, nch = k >> 5, gpr = k >> gsh;
+  uint4* xh = reinterpret_cast<uint4*>(lds4);
+  uint4* xl = xh + 4 * nch;
+  float4* xb = lds4 + 8 * nch;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rp = wave & 3, ks = wave >> 2;  // row pair, K slice
+  const int c0 = (int)(((int64_t)nch * ks) / KS), c1 = (int)(((int64_t)nch * (ks + 1)) / KS);
+  const int o0 = blockIdx.x * kKsRows + 2 * rp;
+
+  // x: XR words a thread, requested first (vector memory completes in order, so waiting for x does not wait for the
+  // weights requested after it)
+  constexpr int XR = 2;  // K <= 2 * 8 * 256 KS
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(x, (uint32_t)k * 4);
+  float4 xa[XR], xc[XR];
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const uint32_t wi = threadIdx.x + 256 * KS * i;
+    const bool ok = wi < (uint32_t)kw;
+    xa[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 : kOOB));
+    xc[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 + 16 : kOOB));
+  }
+  // the two rows' chunks of this slice (rows past the end repeat the last row; their sums are not stored)
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)n_out * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)(((size_t)n_out * gpr * 2 + 3) & ~(size_t)3));
+  uint4 w[CPS][2];
+  uint32_t sc[CPS][2], sh[CPS][2];
+#pragma unroll
+  for (int j = 0; j < CPS; ++j) {
+    const uint32_t c = (uint32_t)(c0 + lane + 64 * j);
+    const bool ok = c < (uint32_t)c1;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t row = (uint32_t)min(o0 + r, n_out - 1);
+      const uint32_t si = row * (uint32_t)gpr + ((32 * c) >> gsh);
+      w[j][r] = buf_load16p<kWPolicy>(w_rsrc, ok ? (row * (uint32_t)kw + 4 * c) * 4 : kOOB);
+      sc[j][r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, ok ? (si * 2) & ~3u : kOOB, 0, 0);
+      sh[j][r] = (si & 1) << 4;
+    }
+  }
+  // the residual (kAdd), requested now rather than after the sums, so its latency is hidden too
+  float yres = 0.f;
+  if constexpr (MODE == kAdd) {
+    const int o = blockIdx.x * kKsRows + (int)threadIdx.x;
+    const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(y, (uint32_t)n_out * 4);
+    yres = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        y_rsrc, threadIdx.x < kKsRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
+  }
+  // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_half needs
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int wi = threadIdx.x + 256 * KS * i;
+    if (wi < kw) stage_half(0, wi >> 2, wi & 3, xa[i], xc[i], xh, xl, xb, nch);
+  }
+  __syncthreads();
+
+  float acc[2][1] = {{0.f}, {0.f}};
+#pragma unroll
+  for (int j = 0; j < CPS; ++j) {
+    const int c = c0 + lane + 64 * j;
+    if (c < c1) {
+      const uint4 wr[2] = {w[j][0], w[j][1]};
+      const uint16_t s16[2] = {(uint16_t)(sc[j][0] >> sh[j][0]), (uint16_t)(sc[j][1] >> sh[j][1])};
+      chunk_dot<2, 1>(xh, xl, xb, nch, c, wr, s16, acc);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const float v = wave_sum(acc[r][0]);
+    if (lane == 0) red[ks][2 * rp + r] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kKsRows) {
+    const int o = blockIdx.x * kKsRows + threadIdx.x;
+    if (o < n_out) {
+      float v = red[0][threadIdx.x];
+#pragma unroll
+      for (int q = 1; q < KS; ++q) v += red[q][threadIdx.x];
+      y[o] = MODE == kAdd ? yres + v : v;
+    }
+  }
+}
+
+// K slices a workgroup of the long-K form (0: not used): 2 at K = 4096, 4 from K = 8192 (64 chunks a slice, one per
+// lane), for at most 4096 outputs (512 workgroups) and K <= 16384.
+inline int gemv_k_slices(int64_t n_out, int64_t k) {
+  if (n_out > 4096 || k < 4096 || k > 16384) return 0;
+  return k < 8192 ? 2 : 4;
+}
+
+template <int KS, int MODE>
+static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
+                     hipStream_t s) {
+  const int cps = ((k / 32 + KS - 1) / KS + 63) / 64;  // chunks a lane
+  const size_t lds = (size_t)k / 32 * 144;               // xh, xl: 64 B a chunk each; xb: 16 B
+  const dim3 grid((unsigned)((n_out + kKsRows - 1) / kKsRows)), block(256 * KS);
+  const int gsh = __builtin_ctz(group);
+  auto go = [&](auto kern) -> int {
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return AQ_ERR_CAPACITY;
+    hipLaunchKernelGGL(kern, grid, block, lds, s, wq, ws, x, y, n_out, k, gsh);
+    return launch_status();
+  };
+  if (cps == 1) return go(k_gemv_q4_ks<KS, 1, MODE>);
+  if (cps == 2) return go(k_gemv_q4_ks<KS, 2, MODE>);
+  return AQ_ERR_SHAPE;
+}
+
 // Workgroups of a launch over n_out outputs, RO per wave: one pass of 4 waves each, at most 1024 (then grid-stride).
 inline int gemv_blocks(int64_t n_out, int ro) {
   const int64_t b = (n_out + 4 * ro - 1) / (4 * ro);
@@ -636,7 +796,15 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
   if (wrows * k / 2 >= ((int64_t)1 << 31) || (int64_t)tokens * n_out * 4 >= ((int64_t)1 << 31)) return AQ_ERR_CAPACITY;
   if (!aligned(wq, 16) || !aligned(x, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (group >= 32 && (group & (group - 1)) == 0)
+  const bool g32 = group >= 32 && (group & (group - 1)) == 0;
+  if constexpr (MODE == kStore || MODE == kAdd) {
+    if (g32 && tokens == 1 && !fz.norm && !fz.cand && !fz.parts) {
+      const int ks = gemv_k_slices(n_out, k);
+      if (ks == 2) return launch_ks<2, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
+      if (ks == 4) return launch_ks<4, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
+    }
+  }
+  if (g32)
     return launch_g<true, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
   return launch_g<false, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
 }

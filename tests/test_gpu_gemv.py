@@ -31,6 +31,8 @@ def test_c0_shape_parity(dev):
     (33, 4096 + 32, 32, 1), (40, 256, 256, 1), (17, 512, 16, 1), (19, 1024, 8, 1), (23, 96, 24, 1),
     (70, 2048, 32, 2), (70, 2048, 64, 3), (65, 1024, 32, 5), (31, 2048, 128, 8), (9, 4096, 32, 8),
     (40, 2048, 32, 9), (33, 1024, 64, 12), (17, 2048, 32, 16), (21, 512, 16, 13),
+    # the long-K form (K split over the waves of a workgroup): 2 or 4 slices, one or two chunks a lane
+    (2048, 8192, 32, 1), (100, 8192, 64, 1), (4096, 4096, 128, 1), (7, 16384, 32, 1), (9, 12288 + 32, 32, 1),
 ])
 def test_kat_bit_exact(dev, n, k, group, tokens):
     """Integer-exact inputs: the GPU result must equal the exact product bit for bit, whatever the sum order."""
@@ -65,12 +67,12 @@ def test_elementwise_error_bound(dev, n, k, group, tokens):
     assert worst <= 1e-3, worst
 
 
-@pytest.mark.parametrize("tokens", [1, 4])
-def test_add_residual(dev, tokens):
-    """gemv_add_q4: y += W x (llama/kernels/gemv_add_q4.mojo:30)."""
+@pytest.mark.parametrize("tokens,k", [(1, 2048), (4, 2048), (1, 8192)])
+def test_add_residual(dev, tokens, k):
+    """gemv_add_q4: y += W x (llama/kernels/gemv_add_q4.mojo:30); K = 8192 is the decode down projection's form."""
     import torch
-    rng = np.random.default_rng(7)
-    n, k, g = 1000, 2048, 64
+    rng = np.random.default_rng(7 + k)
+    n, g = 1000, 64
     wq, ws = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32), \
         (np.abs(rng.standard_normal((n, k // g))) * 0.02 + 1e-3).astype(np.float16)
     x = rng.standard_normal((tokens, k)).astype(np.float32)

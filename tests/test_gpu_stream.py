@@ -15,8 +15,8 @@ def test_stream_read_xor(dev, nbytes, blocks):
     from aq import ops
     rng = np.random.default_rng(nbytes + blocks)
     words = rng.integers(0, 2 ** 32, nbytes // 4, dtype=np.uint32)
-    sink = torch.zeros(ops.STREAM_READ_MAX_BLOCKS, dtype=torch.int32, device=dev)
+    sink = torch.zeros(4 * ops.STREAM_READ_MAX_BLOCKS, dtype=torch.int32, device=dev)
     torch.ops.aq.stream_read(to_dev(words, dev), sink, blocks)
-    used = blocks if blocks else min(1024, -(-(nbytes // 16) // 1024))
+    used = 4 * (blocks if blocks else min(ops.STREAM_READ_MAX_BLOCKS, -(-(nbytes // 16) // 512)))
     got = np.bitwise_xor.reduce(to_np(sink).view(np.uint32)[:used])
     assert got == np.bitwise_xor.reduce(words)
