@@ -4,11 +4,13 @@
 // lfm2/kernels/lk.mojo:38-72,134-167, qwen3moe/kernels/moek.mojo:30-45,200-223,273-281,496-545): per row n,
 //   y[n] = sum over groups of fp16 scale * sum_k ((nib ^ 8) - 8) * x[k], accumulated in fp32.
 //
-// Design (HBM-bound, ~0.5625 B per weight): a 256-thread workgroup stages x (fp32, all tokens) and per-word sums of
-// x in LDS once, then each wave streams R weight rows at a time: every lane takes whole 16-byte, 32-weight chunks of
-// the rows (chunk c = lane, lane + 64, ...), so a wave's loads of one row are 1 KB contiguous, and applies each
-// decoded word to all T tokens. A word is decoded as q + 8 (XOR 0x88888888, byte masks -> v_cvt_f32_ubyte), and
-// 8 * sum(x) is subtracted once per chunk: two VALU ops per weight. Row sums end in a wave reduction.
+// Design (HBM-bound, ~0.5625 B per weight): a 256-thread workgroup stages x (all tokens) in LDS once, then each wave
+// streams R weight rows at a time: every lane takes whole 16-byte, 32-weight chunks of the rows (chunk c = lane,
+// lane + 64, ...), so a wave's loads of one row are 1 KB contiguous, and applies each word to all T tokens. With a
+// power-of-two group >= 32 (one scale per chunk), x is staged as signed 4-bit digits of 22-bit fixed point and every
+// word meets them in v_dot8_i32_i4 as stored (stage_digits, chunk_dot): exact integer chunk sums, ~1 VALU op per
+// weight. Other groups (and the MoE-down mode) decode a word as q + 8 (XOR 0x88888888, byte masks ->
+// v_cvt_f32_ubyte) against fp32 x and subtract 8 * sum(x) once per chunk. Row sums end in a wave reduction.
 #include "aq_common.h"
 #include "aq_moe_decode.h"
 
@@ -17,88 +19,82 @@ namespace aq {
 enum { kStore = 0, kAdd = 1, kGateUp = 2, kMoeGateUp = 3, kMoeDown = 4 };
 
 // x staging of the power-of-two-group products (G >= 32), for word j (x[32c + 8j .. + 7]) of chunk c of token t,
-// a = its first four values, b = the last four. LDS layout (conflict-free for the chunk loop, where lane c reads
-// consecutive 16-byte slots):
-//   xh[t][j][c]   uint4: x[t, 32c + 8j + (0, 4)], (1, 5), (2, 6), (3, 7) as fp16 pairs (the high parts) (T * 4 planes)
-//   xl[t][j][c]   uint4: the same pairs of x - high part (the low parts)                             (T * 4 planes)
-//   xb[t][c]      float4: (bias, 1 / f, -, -): f = the chunk's power-of-two scale (x is staged as f * x, its
-//                 largest magnitude in [2^9, 2^10), so the low parts stay normal fp16, which v_dot2 needs) and
-//                 bias = sum over the chunk of 1032 f x_k (k % 8 even) or 72 f x_k (odd), the magic values' offset
-// The 4 threads of an aligned quad hold the 4 words of one chunk (they exchange maxima and sums by DPP), so whole
-// quads must call it together.
-__device__ __forceinline__ void stage_half(int t, int c, int j, float4 a, float4 b, uint4* __restrict__ xh,
-                                           uint4* __restrict__ xl, float4* __restrict__ xb, int nch) {
-  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+// a = its first four values, b = the last four. Each chunk of 32 values becomes fixed point against its own power of
+// two: X = rint(x 2^sh) with the largest |X| in [2^21, 2^22], written in six signed base-16 digits, X = sum over
+// d < 6 of 16^d D_d, D_d in [-8, 7] (4-bit two's complement, the Q4W code's own format). LDS layout (lane c of the
+// chunk loop reads consecutive 16-byte slots of a plane: conflict-free):
+//   xd[t][d][c]   uint4: digit d of the chunk's words 0..3 (nibble i of word j = digit d of x[32c + 8j + i])
+//   xf[t][c]      float: 2^-sh (NaN when the chunk holds a non-finite x, so the products become NaN)
+// The digits come from the float bits of fma(x, 2^sh, 1.5 * 2^23), which are 0x4B400000 + X for |X| <= 2^22: adding
+// 0x888888 (8 to every digit position, keeping each in 0..15) and XORing it back leaves D_d's 4-bit pattern in nibble
+// d. The 4 threads of an aligned quad hold the 4 words of one chunk (they exchange exponents by DPP), so whole quads
+// must call it together.
+__device__ __forceinline__ uint32_t gather_byte(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3, uint32_t b) {
+  // byte b of p0, p1, p2, p3 as bytes 0, 1, 2, 3 (v_perm_b32: selector 0x0C gives a zero byte)
+  const uint32_t lo = __builtin_amdgcn_perm(p1, p0, 0x0C0C0000u | ((4u + b) << 8) | b);
+  const uint32_t hi = __builtin_amdgcn_perm(p3, p2, (b << 16) | ((4u + b) << 24) | 0x0C0Cu);
+  return lo | hi;
+}
+
+__device__ __forceinline__ void stage_digits(int t, int c, int j, float4 a, float4 b, uint4* __restrict__ xd,
+                                             float* __restrict__ xf, int nch) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   uint32_t e = 0;
 #pragma unroll
   for (int q = 0; q < 8; ++q) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xFFu);
   e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0xB1, 0xF, 0xF, false));
   e = max(e, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)e, 0x4E, 0xF, 0xF, false));
-  const int sh = e ? min(136 - (int)e, 126) : 0;  // max |f x| in [2^9, 2^10)
-  const float f = __uint_as_float((uint32_t)(sh + 127) << 23);
+  // e = the biased exponent of the chunk's largest |x|, which is below 2^(e - 126): 2^(148 - e) brings it below
+  // 2^22. sh stays within [-126, 126] so that 2^sh and 2^-sh are normal floats (chunks below 2^-104 keep fewer bits).
+  const int sh = e ? min(max(148 - (int)e, -126), 126) : 0;
+  const float p2 = __uint_as_float((uint32_t)(sh + 127) << 23);
+  uint32_t z[8];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) v[q] *= f;
-  uint32_t hw[4], lw[4];
+  for (int q = 0; q < 8; ++q) z[q] = (__float_as_uint(fmaf(v[q], p2, 12582912.0f)) - 0x4AB77778u) ^ 0x00888888u;
+  uint4* dst = xd + (size_t)t * 6 * nch + c;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const _Float16 h0 = (_Float16)v[q], h1 = (_Float16)v[q + 4];
-    const _Float16 l0 = (_Float16)(v[q] - (float)h0), l1 = (_Float16)(v[q + 4] - (float)h1);
-    hw[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-    lw[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+  for (int bb = 0; bb < 3; ++bb) {
+    const uint32_t ev = gather_byte(z[0], z[2], z[4], z[6], bb);  // elements 0, 2, 4, 6: digits 2bb, 2bb + 1
+    const uint32_t od = gather_byte(z[1], z[3], z[5], z[7], bb);  // elements 1, 3, 5, 7
+    const uint32_t d0 = (ev & 0x0F0F0F0Fu) | ((od << 4) & 0xF0F0F0F0u);
+    const uint32_t d1 = ((ev >> 4) & 0x0F0F0F0Fu) | (od & 0xF0F0F0F0u);
+    reinterpret_cast<uint32_t*>(dst + (2 * bb) * nch)[j] = d0;
+    reinterpret_cast<uint32_t*>(dst + (2 * bb + 1) * nch)[j] = d1;
   }
-  xh[(t * 4 + j) * nch + c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  xl[(t * 4 + j) * nch + c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  float bias = 1032.0f * ((v[0] + v[2]) + (v[4] + v[6])) + 72.0f * ((v[1] + v[3]) + (v[5] + v[7]));
-  bias += dpp<0xB1>(0.f, bias);
-  bias += dpp<0x4E>(0.f, bias);
-  if (j == 0) xb[t * nch + c] = make_float4(bias, __uint_as_float((uint32_t)(127 - sh) << 23), 0.f, 0.f);
+  if (j == 0) xf[t * nch + c] = e == 0xFFu ? __uint_as_float(0x7FC00000u) : __uint_as_float((uint32_t)(127 - sh) << 23);
 }
 
 // One 32-weight chunk c of R rows (w: their 16 bytes, sc: their fp16 scale bits) against T tokens staged by
-// stage_half: acc[r][t] += scale_r * sum over the chunk of q * x. Each word's 8 codes become 4 fp16 pairs holding
-// the exact values 1024 + n (bits 0-3, 16-19 of the word, and of the word >> 8) or 64 + n (bits 4-7, 20-23),
-// n = stored nibble ^ 8 = q + 8, one v_bitop3 each: ((w ^ 0x8..8) & mask) | magic. Their dot products with the fp16
-// high and low parts of x (v_dot2_f32_f16: exact products, fp32 sums) minus the staged bias sum_k (1032 or 72) x_k
-// leave sum_k q_k x_k.
+// stage_digits: acc[r][t] += scale_r * sum over the chunk of q * x. The Q4W words are used as they are: one
+// v_dot8_i32_i4 (8 products of signed 4-bit values, exact int32 sum) per word and digit, six digits combined as
+// I = sum of 16^d P_d (|I| < 2^30), then acc += I * scale * 2^-sh. About 32 VALU operations a chunk, row and token.
 template <int R, int T>
-__device__ __forceinline__ void chunk_dot(const uint4* __restrict__ xh, const uint4* __restrict__ xl,
-                                          const float4* __restrict__ xb, int nch, int c, const uint4 (&w)[R],
-                                          const uint16_t (&sc)[R], float (&acc)[R][T]) {
-  half2v pr[R][4][4];  // [row][word][pair]
+__device__ __forceinline__ void chunk_dot(const uint4* __restrict__ xd, const float* __restrict__ xf, int nch, int c,
+                                          const uint4 (&w)[R], const uint16_t (&sc)[R], float (&acc)[R][T]) {
+  float s[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t wj = j == 0 ? w[r].x : j == 1 ? w[r].y : j == 2 ? w[r].z : w[r].w;
-      const uint32_t w8 = wj >> 8;
-      pr[r][j][0] = __builtin_bit_cast(half2v, ((wj ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
-      pr[r][j][1] = __builtin_bit_cast(half2v, ((wj ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
-      pr[r][j][2] = __builtin_bit_cast(half2v, ((w8 ^ 0x00080008u) & 0x000F000Fu) | 0x64006400u);
-      pr[r][j][3] = __builtin_bit_cast(half2v, ((w8 ^ 0x00800080u) & 0x00F000F0u) | 0x54005400u);
-    }
+  for (int r = 0; r < R; ++r) s[r] = half_bits_to_float(sc[r]);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    const float4 bw = xb[t * nch + c];
-    float part[R];
+    uint4 d[6];
 #pragma unroll
-    for (int r = 0; r < R; ++r) part[r] = -bw.x;
+    for (int dd = 0; dd < 6; ++dd) d[dd] = xd[(t * 6 + dd) * nch + c];
+    const float f = xf[t * nch + c];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 hi = xh[(t * 4 + j) * nch + c], lo = xl[(t * 4 + j) * nch + c];
-      const half2v h4[4] = {__builtin_bit_cast(half2v, hi.x), __builtin_bit_cast(half2v, hi.y),
-                            __builtin_bit_cast(half2v, hi.z), __builtin_bit_cast(half2v, hi.w)};
-      const half2v l4[4] = {__builtin_bit_cast(half2v, lo.x), __builtin_bit_cast(half2v, lo.y),
-                            __builtin_bit_cast(half2v, lo.z), __builtin_bit_cast(half2v, lo.w)};
+    for (int r = 0; r < R; ++r) {
+      int pd[6];
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+      for (int dd = 0; dd < 6; ++dd) {
+        int q = __builtin_amdgcn_sdot8((int)w[r].x, (int)d[dd].x, 0, false);
+        q = __builtin_amdgcn_sdot8((int)w[r].y, (int)d[dd].y, q, false);
+        q = __builtin_amdgcn_sdot8((int)w[r].z, (int)d[dd].z, q, false);
+        pd[dd] = __builtin_amdgcn_sdot8((int)w[r].w, (int)d[dd].w, q, false);
+      }
+      uint32_t I = (uint32_t)pd[5];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], h4[q], part[r], false);
-          part[r] = __builtin_amdgcn_fdot2(pr[r][j][q], l4[q], part[r], false);
-        }
+      for (int dd = 4; dd >= 0; --dd) I = (I << 4) + (uint32_t)pd[dd];
+      acc[r][t] = fmaf((float)(int)I, s[r] * f, acc[r][t]);
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r][t] = fmaf(part[r], half_bits_to_float(sc[r]) * bw.y, acc[r][t]);
   }
 }
 
@@ -152,7 +148,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
                                                  const float* __restrict__ x, float* __restrict__ y, int n_out,
                                                  int k, int group, int f, int tokens, MoeArgs moe, Fuse fz) {
   // LDS layout, conflict-free for the chunk loop (lane c reads consecutive 16-byte slots). G32 (not kMoeDown): the
-  // xh / xl / xb planes of stage_half. Otherwise:
+  // xd / xf planes of stage_digits. Otherwise:
   //   xs4[t][p][c]  float4 p = 2j + h holds x[t, 32c + 8j + 4h .. + 3]  (T * 8 planes of nch float4)
   //   xsum[t][j][c] sum of x[t, 32c + 8j .. + 7]                        (T * 4 planes of nch floats)
   extern __shared__ float4 lds4[];
@@ -161,11 +157,10 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   const int nch = k >> 5;
   float4* xs4 = lds4;
   float* xsum = reinterpret_cast<float*>(lds4 + T * 8 * nch);
-  uint4* xh = reinterpret_cast<uint4*>(lds4);
-  uint4* xl = xh + T * 4 * nch;
-  float4* xb = lds4 + T * 8 * nch;
-  // fp16-pair products (v_dot2_f32_f16) for the G32 modes but kMoeDown
-  constexpr bool kHalfX = G32 && MODE != kMoeDown;
+  uint4* xd = reinterpret_cast<uint4*>(lds4);
+  float* xf = reinterpret_cast<float*>(xd + T * 6 * nch);
+  // digit products (v_dot8_i32_i4) for the G32 modes but kMoeDown
+  constexpr bool kDigits = G32 && MODE != kMoeDown;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int gpr = k / group;
@@ -182,7 +177,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   // scales travel as raw fp16 bits and are converted where used: a conversion next to its load would wait for it
   const int gsh = __builtin_ctz(group);  // G32 groups are powers of two
   auto use_chunk = [&](int c, const uint4 (&w)[R], const uint16_t (&sc)[R], float (&acc)[R][T]) {
-    chunk_dot<R, T>(xh, xl, xb, nch, c, w, sc, acc);
+    chunk_dot<R, T>(xd, xf, nch, c, w, sc, acc);
   };
 
   // The first chunk of this wave's first row block is requested before x is staged, so its latency overlaps the
@@ -296,8 +291,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       b.z *= half_bits_to_float(wn.w & 0xFFFF);
       b.w *= half_bits_to_float(wn.w >> 16);
     }
-    if constexpr (kHalfX) {
-      stage_half(t, c, j, a, b, xh, xl, xb, nch);
+    if constexpr (kDigits) {
+      stage_digits(t, c, j, a, b, xd, xf, nch);
     } else {
       xs4[(t * 8 + 2 * j) * nch + c] = a;
       xs4[(t * 8 + 2 * j + 1) * nch + c] = b;
@@ -575,7 +570,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 // Long-K products with few rows (one token, power-of-two groups >= 32, no fusions; the decode down projection):
 // KS waves share each pair of rows, each taking 1/KS of K, so N = 2048 outputs over K = 8192 run 16 waves per CU
 // instead of 4 (one workgroup of 256 KS threads per 8 outputs; a plain read of the same bytes by 256 workgroups of
-// 256 threads takes 4.1 us against 3.6 us by 1024). The workgroup stages x once (stage_half); each wave requests
+// 256 threads takes 4.1 us against 3.6 us by 1024). The workgroup stages x once (stage_digits); each wave requests
 // its two rows' chunks of its K slice first, then its words of x, and the KS partial sums of an output meet in LDS,
 // added in slice order.
 constexpr int kKsRows = 8;  // outputs a workgroup: 4 row pairs
@@ -588,9 +583,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
   extern __shared__ float4 lds4[];
   __shared__ float red[KS][kKsRows];
   const int kw = k >> 3, nch = k >> 5, gpr = k >> gsh;
-  uint4* xh = reinterpret_cast<uint4*>(lds4);
-  uint4* xl = xh + 4 * nch;
-  float4* xb = lds4 + 8 * nch;
+  uint4* xd = reinterpret_cast<uint4*>(lds4);
+  float* xf = reinterpret_cast<float*>(xd + 6 * nch);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rp = wave & 3, ks = wave >> 2;  // row pair, K slice
   const int c0 = (int)(((int64_t)nch * ks) / KS), c1 = (int)(((int64_t)nch * (ks + 1)) / KS);
@@ -634,11 +628,11 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
     yres = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         y_rsrc, threadIdx.x < kKsRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
   }
-  // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_half needs
+  // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_digits needs
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
     const int wi = threadIdx.x + 256 * KS * i;
-    if (wi < kw) stage_half(0, wi >> 2, wi & 3, xa[i], xc[i], xh, xl, xb, nch);
+    if (wi < kw) stage_digits(0, wi >> 2, wi & 3, xa[i], xc[i], xd, xf, nch);
   }
   __syncthreads();
 
@@ -649,7 +643,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
     if (c < c1) {
       const uint4 wr[2] = {w[j][0], w[j][1]};
       const uint16_t s16[2] = {(uint16_t)(sc[j][0] >> sh[j][0]), (uint16_t)(sc[j][1] >> sh[j][1])};
-      chunk_dot<2, 1>(xh, xl, xb, nch, c, wr, s16, acc);
+      chunk_dot<2, 1>(xd, xf, nch, c, wr, s16, acc);
     }
   }
 #pragma unroll
@@ -680,7 +674,7 @@ template <int KS, int MODE>
 static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
                      hipStream_t s) {
   const int cps = ((k / 32 + KS - 1) / KS + 63) / 64;  // chunks a lane
-  const size_t lds = (size_t)k / 32 * 144;               // xh, xl: 64 B a chunk each; xb: 16 B
+  const size_t lds = (size_t)k / 32 * 100;               // xd: 6 x 16 B a chunk; xf: 4 B
   const dim3 grid((unsigned)((n_out + kKsRows - 1) / kKsRows)), block(256 * KS);
   const int gsh = __builtin_ctz(group);
   auto go = [&](auto kern) -> int {

@@ -49,9 +49,10 @@ def test_kat_bit_exact(dev, n, k, group, tokens):
                                                 (3000, 2048, 128, 1), (1000, 2048, 32, 4), (700, 1024, 32, 13)])
 def test_elementwise_error_bound(dev, n, k, group, tokens):
     """Every output, not only the largest, within 1e-3 of its own scale: |y - ref| <= 1e-3 * (|W| . |x|) elementwise.
-    The power-of-two-group path sums fp16 magic-offset pairs and cancels the offsets afterwards, so x spans seven
-    decades within and across 32-wide chunks (a small x beside a large one in the same chunk keeps only its fp16
-    low part). The bound is relative to |W| . |x|, not to |y|, so it also holds the rows whose sums nearly cancel."""
+    The power-of-two-group path rounds each 32-wide chunk of x to 22-bit fixed point against the chunk's largest
+    value, so x spans seven decades within and across chunks (a small x beside a large one keeps only the bits above
+    2^-22 of the chunk's maximum). The bound is relative to |W| . |x|, not to |y|, so it also holds the rows whose sums
+    nearly cancel."""
     import torch
     from aq import synth
     rng = np.random.default_rng(n + k + group + tokens)
@@ -136,3 +137,22 @@ def test_few_rows_vs_oracle(dev, tokens, k):
     y = to_dev(y0, dev)
     _ops().gemv_q4(to_dev(wq, dev), to_dev(ws, dev), to_dev(x, dev), y, 32, add=True)
     assert rel_inf(to_np(y), orc.gemm_q4(wq, ws, x, 32, y0=y0)) < TOL_FP32
+
+
+@pytest.mark.parametrize("k,n", [(2048, 300), (8192, 2048)])
+def test_non_finite_x_gives_nan(dev, k, n):
+    """A NaN in x makes every output NaN, as the reference's fp32 sums do (0 * NaN included); the other tokens'
+    outputs stay finite and correct."""
+    import torch
+    rng = np.random.default_rng(k + n)
+    wq = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32)
+    ws = (np.abs(rng.standard_normal((n, k // 32))) * 0.02 + 1e-3).astype(np.float16)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    x[0, k // 3] = np.nan
+    y = torch.empty((2, n), dtype=torch.float32, device=dev)
+    for t in range(2):  # one token at a time: the decode forms
+        yt = y[t]
+        _ops().gemv_q4(to_dev(wq, dev), to_dev(ws, dev), to_dev(x[t], dev), yt, 32)
+    got = to_np(y)
+    assert np.isnan(got[0]).all()
+    assert rel_inf(got[1], orc.gemv_q4(wq, ws, x[1], 32)) < TOL_FP32
