@@ -567,37 +567,37 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   }
 }
 
-// Long-K products with few rows (one token, power-of-two groups >= 32, no fusions; the decode down projection):
-// KS waves share each pair of rows, each taking 1/KS of K, so N = 2048 outputs over K = 8192 run 16 waves per CU
-// instead of 4 (one workgroup of 256 KS threads per 8 outputs; a plain read of the same bytes by 256 workgroups of
-// 256 threads takes 4.1 us against 3.6 us by 1024). The workgroup stages x once (stage_digits); each wave requests
-// its two rows' chunks of its K slice first, then its words of x, and the KS partial sums of an output meet in LDS,
-// added in slice order.
-constexpr int kKsRows = 8;  // outputs a workgroup: 4 row pairs
-
+// One token, power-of-two groups >= 32, no fusions (the decode down projection, and products such as C0's
+// 8192 x 2048): workgroups of 16 waves, so x is staged once per CU instead of once per four-wave workgroup. The 16
+// waves are RP = 16 / KS row pairs times KS slices of K: each wave requests its two rows' chunks of its K slice, then
+// its words of x, and the KS partial sums of an output meet in LDS, added in slice order. KS = 4 (K >= 8192) runs
+// the 2048-row down projection with 16 waves per CU instead of 4 (a plain read of its bytes by 256 workgroups of 256
+// threads takes 4.1 us against 3.6 us by 1024); KS = 1 (32 rows a workgroup) takes C0 from 4.46 to 4.22 us.
 template <int KS, int CPS, int MODE>
-__global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restrict__ wq,
+__global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict__ wq,
                                                          const uint16_t* __restrict__ ws,
                                                          const float* __restrict__ x, float* __restrict__ y,
                                                          int n_out, int k, int gsh) {
+  constexpr int RP = 16 / KS;      // row pairs a workgroup
+  constexpr int kRows = 2 * RP;    // outputs a workgroup
   extern __shared__ float4 lds4[];
-  __shared__ float red[KS][kKsRows];
+  __shared__ float red[KS][kRows];
   const int kw = k >> 3, nch = k >> 5, gpr = k >> gsh;
   uint4* xd = reinterpret_cast<uint4*>(lds4);
   float* xf = reinterpret_cast<float*>(xd + 6 * nch);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rp = wave & 3, ks = wave >> 2;  // row pair, K slice
+  const int rp = wave % RP, ks = wave / RP;  // row pair, K slice
   const int c0 = (int)(((int64_t)nch * ks) / KS), c1 = (int)(((int64_t)nch * (ks + 1)) / KS);
-  const int o0 = blockIdx.x * kKsRows + 2 * rp;
+  const int o0 = blockIdx.x * kRows + 2 * rp;
 
   // x: XR words a thread, requested first (vector memory completes in order, so waiting for x does not wait for the
   // weights requested after it)
-  constexpr int XR = 2;  // K <= 2 * 8 * 256 KS
+  constexpr int XR = 2;  // K <= 2 * 8 * 1024
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(x, (uint32_t)k * 4);
   float4 xa[XR], xc[XR];
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
-    const uint32_t wi = threadIdx.x + 256 * KS * i;
+    const uint32_t wi = threadIdx.x + 1024 * i;
     const bool ok = wi < (uint32_t)kw;
     xa[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 : kOOB));
     xc[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 + 16 : kOOB));
@@ -623,15 +623,15 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
   // the residual (kAdd), requested now rather than after the sums, so its latency is hidden too
   float yres = 0.f;
   if constexpr (MODE == kAdd) {
-    const int o = blockIdx.x * kKsRows + (int)threadIdx.x;
+    const int o = blockIdx.x * kRows + (int)threadIdx.x;
     const __amdgpu_buffer_rsrc_t y_rsrc = make_rsrc(y, (uint32_t)n_out * 4);
     yres = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        y_rsrc, threadIdx.x < kKsRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
+        y_rsrc, threadIdx.x < kRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
   }
   // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_digits needs
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
-    const int wi = threadIdx.x + 256 * KS * i;
+    const int wi = threadIdx.x + 1024 * i;
     if (wi < kw) stage_digits(0, wi >> 2, wi & 3, xa[i], xc[i], xd, xf, nch);
   }
   __syncthreads();
@@ -652,8 +652,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
     if (lane == 0) red[ks][2 * rp + r] = v;
   }
   __syncthreads();
-  if (threadIdx.x < kKsRows) {
-    const int o = blockIdx.x * kKsRows + threadIdx.x;
+  if (threadIdx.x < kRows) {
+    const int o = blockIdx.x * kRows + threadIdx.x;
     if (o < n_out) {
       float v = red[0][threadIdx.x];
 #pragma unroll
@@ -663,9 +663,11 @@ __global__ __launch_bounds__(256 * KS) void k_gemv_q4_ks(const uint32_t* __restr
   }
 }
 
-// K slices a workgroup of the long-K form (0: not used): 2 at K = 4096, 4 from K = 8192 (64 chunks a slice, one per
-// lane), for at most 4096 outputs (512 workgroups) and K <= 16384.
+// K slices a workgroup of the 16-wave form (0: not used): 2 at K = 4096, 4 from K = 8192 (64 chunks a slice, one per
+// lane) for at most 4096 outputs (512 workgroups) and K <= 16384; 1 for 8192 to 32768 outputs over K <= 4096 (256 to
+// 1024 workgroups of 32 outputs).
 inline int gemv_k_slices(int64_t n_out, int64_t k) {
+  if (k <= 4096 && n_out >= 8192 && n_out <= 32768) return 1;
   if (n_out > 4096 || k < 4096 || k > 16384) return 0;
   return k < 8192 ? 2 : 4;
 }
@@ -675,7 +677,8 @@ static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, flo
                      hipStream_t s) {
   const int cps = ((k / 32 + KS - 1) / KS + 63) / 64;  // chunks a lane
   const size_t lds = (size_t)k / 32 * 100;               // xd: 6 x 16 B a chunk; xf: 4 B
-  const dim3 grid((unsigned)((n_out + kKsRows - 1) / kKsRows)), block(256 * KS);
+  const int rows = 32 / KS;  // outputs a workgroup
+  const dim3 grid((unsigned)((n_out + rows - 1) / rows)), block(1024);
   const int gsh = __builtin_ctz(group);
   auto go = [&](auto kern) -> int {
     if (lds > 64 * 1024 &&
@@ -794,6 +797,7 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
   if constexpr (MODE == kStore || MODE == kAdd) {
     if (g32 && tokens == 1 && !fz.norm && !fz.cand && !fz.parts) {
       const int ks = gemv_k_slices(n_out, k);
+      if (ks == 1) return launch_ks<1, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
       if (ks == 2) return launch_ks<2, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
       if (ks == 4) return launch_ks<4, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
     }

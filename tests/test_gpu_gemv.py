@@ -33,6 +33,8 @@ def test_c0_shape_parity(dev):
     (40, 2048, 32, 9), (33, 1024, 64, 12), (17, 2048, 32, 16), (21, 512, 16, 13),
     # the long-K form (K split over the waves of a workgroup): 2 or 4 slices, one or two chunks a lane
     (2048, 8192, 32, 1), (100, 8192, 64, 1), (4096, 4096, 128, 1), (7, 16384, 32, 1), (9, 12288 + 32, 32, 1),
+    # the 16-wave form without a K split (32 outputs a workgroup): C0's shape, a ragged row count, two chunks a lane
+    (8192, 2048, 32, 1), (12000 + 3, 4096, 64, 1), (32768, 1024, 32, 1),
 ])
 def test_kat_bit_exact(dev, n, k, group, tokens):
     """Integer-exact inputs: the GPU result must equal the exact product bit for bit, whatever the sum order."""
