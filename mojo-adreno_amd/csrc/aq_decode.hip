@@ -271,20 +271,22 @@ __global__ __launch_bounds__(kAttnT) void k_attn_decode(const float* __restrict_
 // projection, so the 8 KV heads spread over 8 * splits workgroups with no extra launch.
 //   parts  o: [heads][splits][64] floats, then m, l: [heads][splits][2] floats
 // A split past the last position writes m = -inf, l = 0, o = 0. The split holding pos does RoPE of the key and the
-// cache append (and uses that row from LDS); every split rotates the queries itself. The span's first rows and the
-// q, k, v values are requested before the position is read (they do not depend on it).
+// cache append (and uses that row from registers).
+// Thread t = 8 pg + c owns dimensions 8c .. 8c + 7 of positions s0 + 64 p + pg + 32 i (pass p, i = 0, 1). Everything
+// a wave needs stays in its registers until the end: each lane rotates its own dimensions of the queries (it loads
+// their RoPE partners too), a score is a DPP sum over the 8 lanes of a position, and each wave keeps its own running
+// maximum and rescales its sums when it grows (online softmax), so the only barrier is the final merge of the four
+// waves' states through LDS. The span's first key and value rows and the q, k, v values are requested before the
+// position is read (they do not depend on it).
 template <int HPG>
 __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qkv, const float* __restrict__ cosb,
                                                     const float* __restrict__ sinb, uint16_t* kc, uint16_t* vc,
                                                     const int32_t* __restrict__ pos_p, int heads, int kv_heads,
                                                     int max_pos, int span, float* __restrict__ parts) {
   constexpr int kT = 256;
-  constexpr int kStride = kT / 8;  // 32 positions per pass
-  extern __shared__ float sc[];    // [HPG][span]
-  __shared__ float qs[HPG][kHd];
-  __shared__ float cur[2][kHd];
-  __shared__ float red[kT / 64][HPG];
-  __shared__ float pv[kT / 16][HPG][kHd];
+  constexpr int kStride = kT / 8;  // 32 positions per row of a pass
+  __shared__ float pv[kT / 16][HPG][kHd];  // per (wave, row of 16 lanes) partial outputs
+  __shared__ float2 mls[kT / 64][HPG];     // per wave (m, l)
   const int g = blockIdx.x, sp = blockIdx.y, splits = gridDim.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int s0 = sp * span;
@@ -292,9 +294,6 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
   const size_t cbase = (size_t)g * max_pos * kHd;
   const uint16_t* kbase = kc + cbase + 8 * c;
   const uint16_t* vbase = vc + cbase + 8 * c;
-  // Requests that do not depend on the position go out before it is read: the span's first cached rows (two of each
-  // per thread; rows past the position hold stale values and are masked below, row pos is taken from LDS) and this
-  // head group's q, k, v.
   uint4 kr[2], vr[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -302,12 +301,21 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
     kr[i] = *reinterpret_cast<const uint4*>(kbase + row);
     vr[i] = *reinterpret_cast<const uint4*>(vbase + row);
   }
-  const int qi = t % kHalf;
-  const float* qp = qkv + (size_t)(g * HPG + min(t / kHalf, HPG - 1)) * kHd;
-  const float qa = qp[qi], qb = qp[qi + kHalf];
-  const float* kp = qkv + (size_t)heads * kHd + g * kHd;
-  const float* vp = qkv + (size_t)(heads + kv_heads) * kHd + g * kHd;
-  const float ka = kp[qi], kb = kp[qi + kHalf], va = vp[qi], vb = vp[qi + kHalf];
+  // this lane's 8 dimensions d = 8c + e of q (every head), k and v, and their RoPE partners d +- 32
+  const int d0 = 8 * c, dp = c < 4 ? d0 + kHalf : d0 - kHalf, qi0 = d0 & (kHalf - 1);
+  float4 qa[HPG][2], qb[HPG][2];
+#pragma unroll
+  for (int h = 0; h < HPG; ++h) {
+    const float4* qp = reinterpret_cast<const float4*>(qkv + (size_t)(g * HPG + h) * kHd);
+    qa[h][0] = qp[d0 / 4];
+    qa[h][1] = qp[d0 / 4 + 1];
+    qb[h][0] = qp[dp / 4];
+    qb[h][1] = qp[dp / 4 + 1];
+  }
+  const float4* kp = reinterpret_cast<const float4*>(qkv + (size_t)heads * kHd + g * kHd);
+  const float4* vp = reinterpret_cast<const float4*>(qkv + (size_t)(heads + kv_heads) * kHd + g * kHd);
+  const float4 ka0 = kp[d0 / 4], ka1 = kp[d0 / 4 + 1], kb0 = kp[dp / 4], kb1 = kp[dp / 4 + 1];
+  const float4 va0 = vp[d0 / 4], va1 = vp[d0 / 4 + 1];
   const int pos = *pos_p;
   float* po = parts + (size_t)g * HPG * splits * kHd;                       // o of head g*HPG + h, split sp
   float* pml = parts + (size_t)heads * splits * kHd + (size_t)g * HPG * splits * 2;
@@ -323,46 +331,79 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
   const bool mine = pos < s0 + span;       // holds position pos: rotates and stores its key and value
   const int passes = (s1 - s0 + 2 * kStride - 1) / (2 * kStride);
 
-  const float cs = cosb[pos * kHalf + qi], sn = sinb[pos * kHalf + qi];
-  if (t < HPG * kHalf) {
-    const int hh = t / kHalf;
-    qs[hh][qi] = qa * cs - qb * sn;
-    qs[hh][qi + kHalf] = qb * cs + qa * sn;
+  // RoPE (rotate_half): for d < 32, x'[d] = x[d] cos - x[d + 32] sin; for d >= 32, x'[d] = x[d] cos + x[d - 32] sin
+  float cs[8], sn[8];
+  {
+    const float4* cp = reinterpret_cast<const float4*>(cosb + (size_t)pos * kHalf + qi0);
+    const float4* sq = reinterpret_cast<const float4*>(sinb + (size_t)pos * kHalf + qi0);
+    const float4 c0 = cp[0], c1 = cp[1], q0 = sq[0], q1 = sq[1];
+    const float sgn = c < 4 ? -1.f : 1.f;
+    cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+    sn[0] = sgn * q0.x; sn[1] = sgn * q0.y; sn[2] = sgn * q0.z; sn[3] = sgn * q0.w;
+    sn[4] = sgn * q1.x; sn[5] = sgn * q1.y; sn[6] = sgn * q1.z; sn[7] = sgn * q1.w;
   }
-  if (mine && t >= kT - kHalf) {  // the last 32 threads (with 8 query heads they also rotated a query pair)
-    const int i = qi;
-    const uint16_t k0 = float_to_half_bits(ka * cs - kb * sn), k1 = float_to_half_bits(kb * cs + ka * sn);
-    const uint16_t v0 = float_to_half_bits(va), v1 = float_to_half_bits(vb);
-    uint16_t* kd = kc + cbase + (size_t)pos * kHd;
-    uint16_t* vd = vc + cbase + (size_t)pos * kHd;
-    kd[i] = k0;
-    kd[i + kHalf] = k1;
-    vd[i] = v0;
-    vd[i + kHalf] = v1;
-    cur[0][i] = half_bits_to_float(k0);
-    cur[0][i + kHalf] = half_bits_to_float(k1);
-    cur[1][i] = half_bits_to_float(v0);
-    cur[1][i + kHalf] = half_bits_to_float(v1);
+  auto rope8 = [&](const float4 a0, const float4 a1, const float4 b0, const float4 b1, float (&out)[8]) {
+    const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = a[e] * cs[e] + b[e] * sn[e];
+  };
+  float qr[HPG][8];
+#pragma unroll
+  for (int h = 0; h < HPG; ++h) rope8(qa[h][0], qa[h][1], qb[h][0], qb[h][1], qr[h]);
+  // the key and value of position pos as the cache stores them (fp16), kept in registers for that row
+  float kcur[8], vcur[8];
+  {
+    float kf[8];
+    rope8(ka0, ka1, kb0, kb1, kf);
+    const float vf[8] = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
+    uint32_t kw[4], vw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t k0 = float_to_half_bits(kf[2 * e]), k1 = float_to_half_bits(kf[2 * e + 1]);
+      const uint16_t v0 = float_to_half_bits(vf[2 * e]), v1 = float_to_half_bits(vf[2 * e + 1]);
+      kw[e] = (uint32_t)k0 | ((uint32_t)k1 << 16);
+      vw[e] = (uint32_t)v0 | ((uint32_t)v1 << 16);
+      kcur[2 * e] = half_bits_to_float(k0);
+      kcur[2 * e + 1] = half_bits_to_float(k1);
+      vcur[2 * e] = half_bits_to_float(v0);
+      vcur[2 * e + 1] = half_bits_to_float(v1);
+    }
+    if (mine && pg == 0) {  // eight lanes store the row (16 bytes each)
+      *reinterpret_cast<uint4*>(kc + cbase + (size_t)pos * kHd + d0) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+      *reinterpret_cast<uint4*>(vc + cbase + (size_t)pos * kHd + d0) = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+    }
   }
-  __syncthreads();
 
-  float qr[HPG][8], kcur[8], vcur[8];
+  // online softmax of this wave's positions: m (wave-uniform), and per lane l (lanes c == 0 count each position
+  // once) and the unnormalised output acc over the lane's 8 dimensions
+  float m[HPG], l[HPG], acc[HPG][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int h = 0; h < HPG; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
 #pragma unroll
-    for (int h = 0; h < HPG; ++h) qr[h][e] = qs[h][8 * c + e];
-    kcur[e] = cur[0][8 * c + e];  // read only where s == pos, which only the split holding pos has
-    vcur[e] = cur[1][8 * c + e];
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
   }
-  float m[HPG];
+  for (int p = 0; p < passes; ++p) {
+    const int base = s0 + 2 * kStride * p;
+    uint4 k2[2], v2[2];
+    if (p == 0) {
+      k2[0] = kr[0]; k2[1] = kr[1]; v2[0] = vr[0]; v2[1] = vr[1];
+    } else {
 #pragma unroll
-  for (int h = 0; h < HPG; ++h) m[h] = -INFINITY;
-  auto score_rows = [&](const uint4 (&rows)[2], int base) {
+      for (int i = 0; i < 2; ++i) {
+        const size_t row = (size_t)min(base + pg + kStride * i, pos) * kHd;
+        k2[i] = *reinterpret_cast<const uint4*>(kbase + row);
+        v2[i] = *reinterpret_cast<const uint4*>(vbase + row);
+      }
+    }
+    float sc[2][HPG];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int s = base + pg + kStride * i;
       float k8[8];
-      unpack8(rows[i], k8);
+      unpack8(k2[i], k8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) k8[e] = s == pos ? kcur[e] : k8[e];
 #pragma unroll
@@ -371,105 +412,64 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], k8[e], d);
         const float v = sum8(d) * 0.125f;  // 1 / sqrt(64)
-        if (s < s1) {
-          if (c == 0) sc[h * span + (s - s0)] = v;
-          m[h] = fmaxf(m[h], v);
-        }
+        sc[i][h] = s < s1 ? v : -INFINITY;
       }
     }
-  };
-  score_rows(kr, s0);
-  for (int p = 1; p < passes; ++p) {
-    uint4 k2[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      k2[i] = *reinterpret_cast<const uint4*>(kbase + (size_t)min(s0 + 2 * kStride * p + pg + kStride * i, pos) * kHd);
-    score_rows(k2, s0 + 2 * kStride * p);
-  }
-#pragma unroll
-  for (int h = 0; h < HPG; ++h) {
-    m[h] = wave_max(m[h]);
-    if (lane == 0) red[wave][h] = m[h];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < HPG; ++h) m[h] = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
-  __syncthreads();  // red is reused below
-
-  float l[HPG];
-#pragma unroll
-  for (int h = 0; h < HPG; ++h) l[h] = 0.f;
-  for (int s = t; s < s1 - s0; s += kT) {
 #pragma unroll
     for (int h = 0; h < HPG; ++h) {
-      const float e = expf(sc[h * span + s] - m[h]);
-      sc[h * span + s] = e;
-      l[h] += e;
-    }
-  }
+      const float mn = fmaxf(m[h], wave_max(fmaxf(sc[0][h], sc[1][h])));
+      if (mn == -INFINITY) continue;  // wave-uniform: no position of this wave so far
+      const float r = expf(m[h] - mn);  // 0 while m was -inf
+      const float p0 = expf(sc[0][h] - mn), p1 = expf(sc[1][h] - mn);  // 0 for masked positions
+      l[h] = l[h] * r + (c == 0 ? p0 + p1 : 0.f);
+      m[h] = mn;
+      float v0[8], v1[8];
+      unpack8(v2[0], v0);
+      unpack8(v2[1], v1);
+      const int sa = base + pg, sb = base + pg + kStride;
 #pragma unroll
-  for (int h = 0; h < HPG; ++h) {
-    l[h] = wave_sum(l[h]);
-    if (lane == 0) red[wave][h] = l[h];
-  }
-  __syncthreads();  // also publishes the probabilities
-
-  float acc[HPG][8];
-#pragma unroll
-  for (int h = 0; h < HPG; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-  auto accumulate = [&](const uint4 (&rows)[2], int base) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int s = base + pg + kStride * i;
-      if (s >= s1) break;  // positions rise with i
-      float v8[8];
-      unpack8(rows[i], v8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v8[e] = s == pos ? vcur[e] : v8[e];
-#pragma unroll
-      for (int h = 0; h < HPG; ++h) {
-        const float p = sc[h * span + (s - s0)];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, v8[e], acc[h][e]);
+      for (int e = 0; e < 8; ++e) {
+        const float x0 = sa == pos ? vcur[e] : v0[e], x1 = sb == pos ? vcur[e] : v1[e];
+        acc[h][e] = fmaf(p1, x1, fmaf(p0, x0, acc[h][e] * r));
       }
     }
-  };
-  accumulate(vr, s0);
-  for (int p = 1; p < passes; ++p) {
-    uint4 v2[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      v2[i] = *reinterpret_cast<const uint4*>(vbase + (size_t)min(s0 + 2 * kStride * p + pg + kStride * i, pos) * kHd);
-    accumulate(v2, s0 + 2 * kStride * p);
   }
+  // the wave's state: its 8 position groups' sums (lanes l, l ^ 8 by DPP, then the 4 rows through LDS), m, and l
 #pragma unroll
-  for (int h = 0; h < HPG; ++h)
+  for (int h = 0; h < HPG; ++h) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] += dpp<0x128>(0.f, acc[h][e]);  // lanes l, l ^ 8: neighbouring groups
+    const float lw = wave_sum(l[h]);
+    if (lane == 0) mls[wave][h] = make_float2(m[h], lw);
+  }
   if ((lane & 8) == 0) {
     const int row = lane >> 4;
 #pragma unroll
     for (int h = 0; h < HPG; ++h) {
-      float4* dst = reinterpret_cast<float4*>(&pv[wave * 4 + row][h][8 * c]);
+      float4* dst = reinterpret_cast<float4*>(&pv[wave * 4 + row][h][d0]);
       dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
       dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
     }
   }
   __syncthreads();
+  // merge the four waves: M = max m_w, o = sum_w e^(m_w - M) o_w, l = sum_w e^(m_w - M) l_w
   for (int i = t; i < HPG * kHd; i += kT) {
     const int h = i / kHd, d = i % kHd;
-    float v = 0.f;
+    float mw = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kT / 16; ++w) v += pv[w][h][d];
+    for (int w = 0; w < kT / 64; ++w) mw = fmaxf(mw, mls[w][h].x);
+    float v = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kT / 64; ++w) {
+      const float f = mls[w][h].x == -INFINITY ? 0.f : expf(mls[w][h].x - mw);
+      const float ow = (pv[4 * w][h][d] + pv[4 * w + 1][h][d]) + (pv[4 * w + 2][h][d] + pv[4 * w + 3][h][d]);
+      v = fmaf(f, ow, v);
+      lt = fmaf(f, mls[w][h].y, lt);
+    }
     po[(h * splits + sp) * kHd + d] = v;
-  }
-#pragma unroll
-  for (int h = 0; h < HPG; ++h) {
-    if (t == h) {
-      pml[(h * splits + sp) * 2] = m[h];
-      pml[(h * splits + sp) * 2 + 1] = red[0][h] + red[1][h] + red[2][h] + red[3][h];
+    if (d == 0) {
+      pml[(h * splits + sp) * 2] = mw;
+      pml[(h * splits + sp) * 2 + 1] = lt;
     }
   }
 }
@@ -479,7 +479,7 @@ static int launch_split(const float* qkv, const float* cosb, const float* sinb, 
                         const int32_t* pos, int heads, int kv_heads, int max_pos, int splits, float* parts,
                         hipStream_t s) {
   const int span = ((max_pos + splits - 1) / splits + 63) / 64 * 64;
-  hipLaunchKernelGGL(k_attn_split<HPG>, dim3(kv_heads, splits), dim3(256), (size_t)HPG * span * sizeof(float), s,
+  hipLaunchKernelGGL(k_attn_split<HPG>, dim3(kv_heads, splits), dim3(256), 0, s,
                      qkv, cosb, sinb, kc, vc, pos, heads, kv_heads, max_pos, span, parts);
   return launch_status();
 }
