@@ -7,12 +7,14 @@
 //   expert and stages only that slot's activations (a KB each), not all eight;
 // - 8 lanes a row: lane (row r = l / 8, sub = l % 8) takes the 32-weight chunks c = 8 j + sub, j < CPL, of its row
 //   (CPL = f / 256 rounded up: 3 at f = 768, so every lane is busy), all requested at once; the slot's activations
-//   (CPL float4 a lane) are requested before them, so the staging overlaps the weights' flight;
-// - a chunk is 4 words decoded as q + 8 (XOR 0x88888888, byte masks, v_cvt_f32_ubyte) against fp32 activations from
-//   LDS, minus 8 * (the chunk's sum of a), times its fp16 scale (one per chunk: a power-of-two group >= 32);
+//   (a word of 8 values a lane and pass) are requested before them, so the staging overlaps the weights' flight;
+// - the slot's activations are staged as signed 4-bit digits of per-chunk fixed point (stage_digits), and a chunk's
+//   four words meet them in v_dot8_i32_i4 as stored (chunk_dot), times its fp16 scale (one per chunk: a power-of-two
+//   group >= 32);
 // - each row's 8 lane sums meet by DPP, and the 8 slots' sums by LDS: thread r < RW folds them in slot order, so the
 //   result does not depend on scheduling.
 #include "aq_common.h"
+#include "aq_digits.h"
 #include "aq_moe_decode.h"
 
 namespace aq {
@@ -25,27 +27,29 @@ __global__ __launch_bounds__(512) void k_moe_down_dec(const uint32_t* __restrict
                                                       const int32_t* __restrict__ ids, const float* __restrict__ rw,
                                                       const float* __restrict__ act, float* __restrict__ y, int d,
                                                       int f, int gsh, int experts, int topk, int add) {
-  extern __shared__ float4 xs4[];  // [slot][f / 4] activations, then [slot][f / 32] chunk sums
+  extern __shared__ uint4 xd[];  // stage_digits planes of the 8 slots ([slot][6][f / 32]), then their factors
   __shared__ float red[kDownSlots][kDownRows];
   const int lane = threadIdx.x & 63;
   const int s = threadIdx.x >> 6;  // expert slot of this wave
   const int r0 = blockIdx.x * kDownRows;
   const int row = lane >> 3, sub = lane & 7;
   const int kw = f >> 3, nch = f >> 5, gpr = f >> gsh;
-  float* csum = reinterpret_cast<float*>(xs4 + kDownSlots * (f >> 2));
+  float* xf = reinterpret_cast<float*>(xd + kDownSlots * 6 * nch);
 
-  // this slot's activations first: they do not depend on the expert id, so their arrival (and the staging below)
-  // overlaps the id's load and the weights' flight; vector memory completes in order, so waiting for them does not
-  // wait for the weights requested after them
-  float4 xr[CPL];
+  // this slot's activations first, a word (8 values) a lane and pass: they do not depend on the expert id, so their
+  // arrival (and the staging below) overlaps the id's load and the weights' flight; vector memory completes in
+  // order, so waiting for them does not wait for the weights requested after them
+  constexpr int XP = (CPL * 8 * 4 + 63) / 64;  // passes: f / 8 words over 64 lanes (f <= 256 CPL)
+  float4 xa[XP], xb[XP];
   const bool slot = s < topk;  // wave-uniform
   {
     const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(act, (uint32_t)topk * (uint32_t)f * 4u);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const uint32_t i = (uint32_t)(lane + 64 * j);  // float4 index within the slot's row
-      xr[j] = __builtin_bit_cast(float4, buf_load16(a_rsrc, slot && i < (uint32_t)(f >> 2)
-                                                                ? ((uint32_t)s * (uint32_t)f + 4u * i) * 4u : kOOB));
+    for (int j = 0; j < XP; ++j) {
+      const uint32_t wi = (uint32_t)(lane + 64 * j);  // word within the slot's row
+      const uint32_t off = slot && wi < (uint32_t)kw ? ((uint32_t)s * (uint32_t)f + 8u * wi) * 4u : kOOB;
+      xa[j] = __builtin_bit_cast(float4, buf_load16(a_rsrc, off));
+      xb[j] = __builtin_bit_cast(float4, buf_load16(a_rsrc, off == kOOB ? kOOB : off + 16u));
     }
   }
   const int e = slot ? ids[s] : -1;
@@ -69,44 +73,31 @@ __global__ __launch_bounds__(512) void k_moe_down_dec(const uint32_t* __restrict
     sh[j] = (si & 1u) << 4;
   }
 
-  // stage them with their chunk sums (8 consecutive float4 = one chunk = 8 consecutive lanes; f % 32 == 0, so a
-  // round holds whole chunks and a chunk's 8 lanes are all in range or all out)
-  float4* xw = xs4 + s * (f >> 2);
+  // stage the slot's digits (f % 32 == 0: kw % 4 == 0, so a pass holds whole chunks and a chunk's 4 lanes are all in
+  // range or all out, as stage_digits needs)
   if (live) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int i = lane + 64 * j;
-      if (i < (f >> 2)) {
-        const float4 v = xr[j];
-        xw[i] = v;
-        const float t = sum8((v.x + v.y) + (v.z + v.w));
-        if ((i & 7) == 0) csum[s * nch + (i >> 3)] = t;
-      }
+    for (int j = 0; j < XP; ++j) {
+      const int wi = lane + 64 * j;
+      if (wi < kw) stage_digits(s, wi >> 2, wi & 3, xa[j], xb[j], xd, xf, nch);
     }
   }
   __syncthreads();
 
-  float acc = 0.f;
+  float acc[1][1] = {{0.f}};
   if (live) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = 8 * j + sub;
       if (c < nch) {
-        const uint32_t wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-        float part = -8.0f * csum[s * nch + c];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float xv[8];
-          *reinterpret_cast<float4*>(xv) = xw[8 * c + 2 * q];
-          *reinterpret_cast<float4*>(xv + 4) = xw[8 * c + 2 * q + 1];
-          part += dot8_biased(wv[q], xv);
-        }
-        acc = fmaf(part, half_bits_to_float((uint16_t)(sc[j] >> sh[j])), acc);
+        const uint4 wr[1] = {w[j]};
+        const uint16_t s16[1] = {(uint16_t)(sc[j] >> sh[j])};
+        chunk_dot<1, 1>(xd + s * 6 * nch, xf + s * nch, nch, c, wr, s16, acc);
       }
     }
   }
-  acc = sum8(acc);
-  if (sub == 0) red[s][row] = live ? acc : 0.f;
+  const float a = sum8(acc[0][0]);
+  if (sub == 0) red[s][row] = live ? a : 0.f;
   __syncthreads();
   if (threadIdx.x < kDownRows) {
     const int o = r0 + threadIdx.x;
@@ -127,7 +118,7 @@ int launch_moe_down_dec(const uint32_t* wq, const uint16_t* ws, const int32_t* i
                         const float* act, float* y, int64_t d, int64_t f, int32_t group, int32_t experts,
                         int32_t topk, int32_t add, hipStream_t st) {
   const int cpl = (int)((f / 32 + 7) / 8);
-  const size_t lds = (size_t)kDownSlots * (size_t)f * 4 + (size_t)kDownSlots * (size_t)(f / 32) * 4;
+  const size_t lds = (size_t)kDownSlots * (size_t)(f / 32) * (6 * 16 + 4);  // digit planes and factors
   const dim3 grid((unsigned)((d + kDownRows - 1) / kDownRows)), block(512);
   const int gsh = __builtin_ctz(group);
 #define AQ_DOWN_CASE(C)                                                                                              \
