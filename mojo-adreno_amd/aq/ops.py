@@ -461,7 +461,8 @@ for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route
 
 # ---- Llama decode step: fused norms, embedding, attention, lm_head + argmax -----------------------------------------
 
-HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax keys of the lm_head launch
+HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax key slots of a head launch (the int4 head keeps its arrival counter
+#                         in the last one: allocate zero-filled)
 ATTN_MAX_SPLITS = 8     # AQ_ATTN_MAX_SPLITS
 
 

@@ -95,6 +95,10 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 // GEMV triple 21.8 -> 21.2 us, the ternary head 35.8 -> 34.1 us (sc1 | nt and sc0 | nt measured the same). Not for
 // loads whose pieces share cache lines (the Q6_K head).
 constexpr int kWPolicy = 2;
+// Device-coherent (sc1) buffer accesses: a store written through to where every XCD reads it, a load that does not
+// take a line an XCD's L2 may hold stale. For data one workgroup hands to another within a launch, with a device-scope
+// atomic ordering the two (no cache writeback needed).
+constexpr int kSc1 = 16;
 template <int POL>
 __device__ __forceinline__ uint4 buf_load16p(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);

@@ -34,12 +34,23 @@ struct MoeArgs {
 // each wave also leaves the largest output it wrote and its row, as an argmax key (cand[block * 4 + wave]).
 // parts != NULL (one token): x is the attention output combined from `splits` partial softmax states (the layout of
 // aq_attn_decode_split): x[h * 64 + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
+// cand != NULL also ends the greedy step in the same launch: each workgroup leaves its best key in cand[block] and
+// counts itself on `arrivals`; the one that arrives last (every other key is then stored) takes the largest key and
+// writes *token, hist[*pos] and *pos += advance, then sets the counter back to zero. The keys are stored and read
+// with device-coherent (sc1) accesses and the counter is a device-scope atomic, so no cache writeback is needed.
 struct Fuse {
   const uint16_t* norm;
   float eps;
   uint64_t* cand;
   const float* parts;
   int splits;
+  // with cand: the greedy step's outputs, and the arrival counter (a 32-bit word, zero between launches)
+  int32_t* token;
+  int32_t* pos;
+  int32_t* hist;
+  int hist_cap;
+  int advance;
+  uint32_t* arrivals;
 };
 
 
@@ -483,8 +494,43 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     finish(base, acc);
   }
   if constexpr (MODE == kStore) {
-    if (fz.cand && lane == 0)
-      fz.cand[blockIdx.x * 4 + wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
+    if (fz.cand) {  // workgroup-uniform
+      __shared__ uint64_t wkey[4];
+      __shared__ int last;
+      if (lane == 0) wkey[wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
+      __syncthreads();
+      const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(fz.cand, gridDim.x * 8u);
+      if (threadIdx.x == 0) {
+        uint64_t m = wkey[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) m = wkey[w] > m ? wkey[w] : m;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, m), c_rsrc, blockIdx.x * 8u, 0, kSc1);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the key has reached device scope
+        last = __hip_atomic_fetch_add(fz.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+      }
+      __syncthreads();
+      if (last) {  // workgroup-uniform: every workgroup's key is stored
+        uint64_t m = 0;
+        for (uint32_t i = threadIdx.x; i < gridDim.x; i += 256) {
+          const uint64_t c = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(c_rsrc, i * 8u, 0, kSc1));
+          m = c > m ? c : m;
+        }
+        m = wave_max_u64(m);
+        if (lane == 0) wkey[wave] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+          for (int w = 1; w < 4; ++w) m = wkey[w] > m ? wkey[w] : m;
+          const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
+          const int p = *fz.pos;
+          *fz.token = idx;
+          if (fz.hist && p >= 0 && p < fz.hist_cap) fz.hist[p] = idx;
+          *fz.pos = p + fz.advance;
+          __hip_atomic_store(fz.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
   }
 }
 
@@ -829,14 +875,19 @@ extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const f
                                  int32_t advance, void* stream) {
   if (!cand || !token || !pos) return AQ_ERR_NULL;
   if (vocab <= 0 || vocab > (int64_t)1 << 30 || hist_cap < 0) return AQ_ERR_SHAPE;
-  const int ncand = 4 * aq::gemv_blocks(vocab, aq::rows_per_wave(vocab));
-  if (cand_cap < ncand) return AQ_ERR_CAPACITY;
+  // one key per workgroup, and the arrival counter in the last slot
+  const int ncand = aq::gemv_blocks(vocab, aq::rows_per_wave(vocab));
+  if (cand_cap < ncand + 1) return AQ_ERR_CAPACITY;
   if (!aq::aligned(cand, 8)) return AQ_ERR_ALIGN;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
-  const int st = aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream,
-                                            aq::Fuse{norm_w, eps, cand, nullptr, 0});
-  if (st != AQ_OK) return st;
-  return aq::launch_argmax_step(cand, ncand, token, pos, hist, hist_cap, advance, reinterpret_cast<hipStream_t>(stream));
+  aq::Fuse fz{norm_w, eps, cand, nullptr, 0};
+  fz.token = token;
+  fz.pos = pos;
+  fz.hist = hist;
+  fz.hist_cap = hist_cap;
+  fz.advance = advance;
+  fz.arrivals = reinterpret_cast<uint32_t*>(cand + (cand_cap - 1));
+  return aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream, fz);
 }
 
 extern "C" int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, int32_t splits, float* y,

@@ -133,6 +133,43 @@ def test_head_argmax(dev, vocab):
     assert h[5] == best and (np.delete(h, 5) == -1).all()
 
 
+def test_head_argmax_one_launch_repeats(dev):
+    """The head ends the greedy step in its own launch (the last workgroup to arrive picks the token): the arrival
+    counter in cand's last slot is back at zero after every call, so calls in a row, eager and replayed from one
+    graph, each give the oracle's token and advance the position."""
+    import torch
+    rng = np.random.default_rng(77)
+    vocab, k = 50000, 2048
+    wq, ws = _int4(rng, vocab, k)
+    xs = [rng.standard_normal(k).astype(np.float32) for _ in range(3)]
+    logits = torch.empty(vocab, dtype=torch.float32, device=dev)
+    cand = torch.zeros(4096, dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.full((8,), -1, dtype=torch.int32, device=dev)
+    nonorm = torch.empty(0, dtype=torch.float16, device=dev)
+    W, S = to_dev(wq, dev), to_dev(ws, dev)
+    x = torch.empty(k, dtype=torch.float32, device=dev)
+    want = [orc.argmax_first(orc.gemv_q4(wq, ws, xv, 32)) for xv in xs]
+    run = lambda: torch.ops.aq.head_argmax_q4(W, S, x, nonorm, 1e-5, logits, 32, cand, tok, pos, hist, 1)  # noqa
+    for i, xv in enumerate(xs):  # eager
+        x.copy_(to_dev(xv, dev))
+        run()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert int(to_np(cand)[-1]) == 0
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    pos.zero_()
+    for i, xv in enumerate(xs):  # replays
+        x.copy_(to_dev(xv, dev))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert int(to_np(cand)[-1]) == 0
+    np.testing.assert_array_equal(to_np(hist)[:3], np.array(want, np.int32))
+
+
 def test_head_argmax_ties_pick_the_first(dev):
     """Rows 3, 40 and 900 are identical and give the largest logit: the token is 3 (integer-exact inputs, no norm)."""
     import torch
