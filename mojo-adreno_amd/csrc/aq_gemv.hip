@@ -540,26 +540,36 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
 // its words of x, and the KS partial sums of an output meet in LDS, added in slice order. KS = 4 (K >= 8192) runs
 // the 2048-row down projection with 16 waves per CU instead of 4 (a plain read of its bytes by 256 workgroups of 256
 // threads takes 4.1 us against 3.6 us by 1024); KS = 1 (32 rows a workgroup) takes C0 from 4.46 to 4.22 us.
-template <int KS, int CPS, int MODE>
+template <int KS, int CPS, int MODE, bool NORM>
 __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict__ wq,
                                                          const uint16_t* __restrict__ ws,
                                                          const float* __restrict__ x, float* __restrict__ y,
-                                                         int n_out, int k, int gsh) {
-  constexpr int RP = 16 / KS;      // row pairs a workgroup
-  constexpr int kRows = 2 * RP;    // outputs a workgroup
+                                                         int n_out, int k, int gsh, int f,
+                                                         const uint16_t* __restrict__ norm, float eps) {
+  constexpr int RP = 16 / KS;                              // row pairs a workgroup
+  constexpr int kRows = MODE == kGateUp ? RP : 2 * RP;     // outputs a workgroup (gate|up: one per row pair)
   extern __shared__ float4 lds4[];
-  __shared__ float red[KS][kRows];
+  __shared__ float red[KS][2 * RP];
+  __shared__ float rss[16];
   const int kw = k >> 3, nch = k >> 5, gpr = k >> gsh;
   uint4* xd = reinterpret_cast<uint4*>(lds4);
   float* xf = reinterpret_cast<float*>(xd + 6 * nch);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rp = wave % RP, ks = wave / RP;  // row pair, K slice
   const int c0 = (int)(((int64_t)nch * ks) / KS), c1 = (int)(((int64_t)nch * (ks + 1)) / KS);
-  const int o0 = blockIdx.x * kRows + 2 * rp;
 
-  // x: XR words a thread, requested first (vector memory completes in order, so waiting for x does not wait for the
-  // weights requested after it)
+  // norm weights first, then x: XR words a thread, requested before the weights (vector memory completes in order,
+  // so waiting for x does not wait for the weights requested after it)
   constexpr int XR = 2;  // K <= 2 * 8 * 1024
+  uint4 xn[XR];
+  if constexpr (NORM) {
+    const __amdgpu_buffer_rsrc_t n_rsrc = make_rsrc(norm, (uint32_t)k * 2);
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+      const uint32_t wi = threadIdx.x + 1024 * i;
+      xn[i] = buf_load16(n_rsrc, wi < (uint32_t)kw ? wi * 16 : kOOB);
+    }
+  }
   const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(x, (uint32_t)k * 4);
   float4 xa[XR], xc[XR];
 #pragma unroll
@@ -569,9 +579,21 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
     xa[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 : kOOB));
     xc[i] = __builtin_bit_cast(float4, buf_load16(x_rsrc, ok ? wi * 32 + 16 : kOOB));
   }
-  // the two rows' chunks of this slice (rows past the end repeat the last row; their sums are not stored)
-  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)((size_t)n_out * kw * 4));
-  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)(((size_t)n_out * gpr * 2 + 3) & ~(size_t)3));
+  // the pair's two rows (gate|up: gate row o and up row f + o; otherwise outputs o0, o0 + 1), their chunks of this
+  // slice; rows past the end repeat the last row, and their sums are not stored
+  uint32_t rows[2];
+  if constexpr (MODE == kGateUp) {
+    const int o = min((int)blockIdx.x * RP + rp, n_out - 1);
+    rows[0] = (uint32_t)o;
+    rows[1] = (uint32_t)(f + o);
+  } else {
+    const int o0 = blockIdx.x * kRows + 2 * rp;
+    rows[0] = (uint32_t)min(o0, n_out - 1);
+    rows[1] = (uint32_t)min(o0 + 1, n_out - 1);
+  }
+  const size_t wrows = MODE == kGateUp ? 2 * (size_t)f : (size_t)n_out;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(wq, (uint32_t)(wrows * kw * 4));
+  const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(ws, (uint32_t)((wrows * gpr * 2 + 3) & ~(size_t)3));
   uint4 w[CPS][2];
   uint32_t sc[CPS][2], sh[CPS][2];
 #pragma unroll
@@ -580,9 +602,8 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
     const bool ok = c < (uint32_t)c1;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint32_t row = (uint32_t)min(o0 + r, n_out - 1);
-      const uint32_t si = row * (uint32_t)gpr + ((32 * c) >> gsh);
-      w[j][r] = buf_load16p<kWPolicy>(w_rsrc, ok ? (row * (uint32_t)kw + 4 * c) * 4 : kOOB);
+      const uint32_t si = rows[r] * (uint32_t)gpr + ((32 * c) >> gsh);
+      w[j][r] = buf_load16p<kWPolicy>(w_rsrc, ok ? (rows[r] * (uint32_t)kw + 4 * c) * 4 : kOOB);
       sc[j][r] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, ok ? (si * 2) & ~3u : kOOB, 0, 0);
       sh[j][r] = (si & 1) << 4;
     }
@@ -595,11 +616,32 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
     yres = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         y_rsrc, threadIdx.x < kRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
   }
-  // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_digits needs
+  // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_digits needs. With a norm, x * norm_w is
+  // staged and sum(x^2) gathered; the sums are scaled by 1 / sqrt(mean(x^2) + eps) at the end (RMSNorm).
+  float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
     const int wi = threadIdx.x + 1024 * i;
-    if (wi < kw) stage_digits(0, wi >> 2, wi & 3, xa[i], xc[i], xd, xf, nch);
+    if (wi < kw) {
+      float4 a = xa[i], b = xc[i];
+      if constexpr (NORM) {
+        ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) + ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+        const uint4 wn = xn[i];
+        a.x *= half_bits_to_float(wn.x & 0xFFFF);
+        a.y *= half_bits_to_float(wn.x >> 16);
+        a.z *= half_bits_to_float(wn.y & 0xFFFF);
+        a.w *= half_bits_to_float(wn.y >> 16);
+        b.x *= half_bits_to_float(wn.z & 0xFFFF);
+        b.y *= half_bits_to_float(wn.z >> 16);
+        b.z *= half_bits_to_float(wn.w & 0xFFFF);
+        b.w *= half_bits_to_float(wn.w >> 16);
+      }
+      stage_digits(0, wi >> 2, wi & 3, a, b, xd, xf, nch);
+    }
+  }
+  if constexpr (NORM) {
+    const float v = wave_sum(ss);
+    if (lane == 0) rss[wave] = v;
   }
   __syncthreads();
 
@@ -622,18 +664,37 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
   if (threadIdx.x < kRows) {
     const int o = blockIdx.x * kRows + threadIdx.x;
     if (o < n_out) {
-      float v = red[0][threadIdx.x];
+      float rs = 1.f;
+      if constexpr (NORM) {
+        float t = 0.f;
 #pragma unroll
-      for (int q = 1; q < KS; ++q) v += red[q][threadIdx.x];
-      y[o] = MODE == kAdd ? yres + v : v;
+        for (int q = 0; q < 16; ++q) t += rss[q];
+        rs = 1.0f / sqrtf(t / (float)k + eps);
+      }
+      if constexpr (MODE == kGateUp) {
+        float g = red[0][2 * threadIdx.x], u = red[0][2 * threadIdx.x + 1];
+#pragma unroll
+        for (int q = 1; q < KS; ++q) {
+          g += red[q][2 * threadIdx.x];
+          u += red[q][2 * threadIdx.x + 1];
+        }
+        y[o] = silu(g * rs) * (u * rs);
+      } else {
+        float v = red[0][threadIdx.x];
+#pragma unroll
+        for (int q = 1; q < KS; ++q) v += red[q][threadIdx.x];
+        y[o] = MODE == kAdd ? yres + v * rs : v * rs;
+      }
     }
   }
 }
 
-// K slices a workgroup of the 16-wave form (0: not used): 2 at K = 4096, 4 from K = 8192 (64 chunks a slice, one per
-// lane) for at most 4096 outputs (512 workgroups) and K <= 16384; 1 for 8192 to 32768 outputs over K <= 4096 (256 to
-// 1024 workgroups of 32 outputs).
-inline int gemv_k_slices(int64_t n_out, int64_t k) {
+// K slices a workgroup of the 16-wave form (0: not used), over n_out outputs: 2 at K = 4096, 4 from K = 8192 (64
+// chunks a slice, one per lane) for at most 4096 outputs (512 workgroups) and K <= 16384; 1 for 8192 to 32768
+// outputs over K <= 4096 (256 to 1024 workgroups of 32 outputs), and for gate|up products of 4096 to 16384 outputs
+// over K <= 4096 (256 to 1024 workgroups of 16 outputs).
+inline int gemv_k_slices(int64_t n_out, int64_t k, bool gate_up) {
+  if (gate_up) return k <= 4096 && n_out >= 4096 && n_out <= 16384 ? 1 : 0;
   if (k <= 4096 && n_out >= 8192 && n_out <= 32768) return 1;
   if (n_out > 4096 || k < 4096 || k > 16384) return 0;
   return k < 8192 ? 2 : 4;
@@ -641,10 +702,10 @@ inline int gemv_k_slices(int64_t n_out, int64_t k) {
 
 template <int KS, int MODE>
 static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int n_out, int k, int group,
-                     hipStream_t s) {
+                     int f, const uint16_t* norm, float eps, hipStream_t s) {
   const int cps = ((k / 32 + KS - 1) / KS + 63) / 64;  // chunks a lane
   const size_t lds = (size_t)k / 32 * 100;               // xd: 6 x 16 B a chunk; xf: 4 B
-  const int rows = 32 / KS;  // outputs a workgroup
+  const int rows = (MODE == kGateUp ? 16 : 32) / KS;    // outputs a workgroup
   const dim3 grid((unsigned)((n_out + rows - 1) / rows)), block(1024);
   const int gsh = __builtin_ctz(group);
   auto go = [&](auto kern) -> int {
@@ -652,11 +713,16 @@ static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, flo
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
       return AQ_ERR_CAPACITY;
-    hipLaunchKernelGGL(kern, grid, block, lds, s, wq, ws, x, y, n_out, k, gsh);
+    hipLaunchKernelGGL(kern, grid, block, lds, s, wq, ws, x, y, n_out, k, gsh, f, norm, eps);
     return launch_status();
   };
-  if (cps == 1) return go(k_gemv_q4_ks<KS, 1, MODE>);
-  if (cps == 2) return go(k_gemv_q4_ks<KS, 2, MODE>);
+  if (norm) {
+    if (cps == 1) return go(k_gemv_q4_ks<KS, 1, MODE, true>);
+    if (cps == 2) return go(k_gemv_q4_ks<KS, 2, MODE, true>);
+  } else {
+    if (cps == 1) return go(k_gemv_q4_ks<KS, 1, MODE, false>);
+    if (cps == 2) return go(k_gemv_q4_ks<KS, 2, MODE, false>);
+  }
   return AQ_ERR_SHAPE;
 }
 
@@ -761,12 +827,13 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
   if (!aligned(wq, 16) || !aligned(x, 16)) return AQ_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool g32 = group >= 32 && (group & (group - 1)) == 0;
-  if constexpr (MODE == kStore || MODE == kAdd) {
-    if (g32 && tokens == 1 && !fz.norm && !fz.cand && !fz.parts) {
-      const int ks = gemv_k_slices(n_out, k);
-      if (ks == 1) return launch_ks<1, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
-      if (ks == 2) return launch_ks<2, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
-      if (ks == 4) return launch_ks<4, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, s);
+  if constexpr (MODE == kStore || MODE == kAdd || MODE == kGateUp) {
+    if (g32 && tokens == 1 && !fz.cand && !fz.parts) {
+      const int ks = gemv_k_slices(n_out, k, MODE == kGateUp);
+      const int fi = (int)f;
+      if (ks == 1) return launch_ks<1, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, fi, fz.norm, fz.eps, s);
+      if (ks == 2) return launch_ks<2, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, fi, fz.norm, fz.eps, s);
+      if (ks == 4) return launch_ks<4, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, fi, fz.norm, fz.eps, s);
     }
   }
   if (g32)

@@ -22,7 +22,8 @@ def _int4(rng, n, k, group=32):
     return synth.int4_matrix(rng, n, k, group)
 
 
-@pytest.mark.parametrize("n,k,tokens", [(3072, 2048, 1), (2048, 8192, 1), (500, 1024, 3)])
+@pytest.mark.parametrize("n,k,tokens", [(3072, 2048, 1), (2048, 8192, 1), (500, 1024, 3), (8192 + 3, 2048, 1),
+                                         (9000, 4096, 1)])
 def test_rmsnorm_gemv(dev, n, k, tokens):
     import torch
     rng = np.random.default_rng(n + k + tokens)
@@ -35,10 +36,12 @@ def test_rmsnorm_gemv(dev, n, k, tokens):
     assert rel_inf(to_np(y), ref) < TOL
 
 
-def test_rmsnorm_gate_up(dev):
+@pytest.mark.parametrize("f,k", [(8192, 2048), (4096 + 5, 2048), (5000, 4096), (768, 2048)])
+def test_rmsnorm_gate_up(dev, f, k):
+    """The decode gate|up with RMSNorm and SwiGLU; 4096 outputs and more take the 16-wave form (16 outputs a
+    workgroup: a ragged count, and two chunks a lane at K = 4096), fewer the four-wave form."""
     import torch
-    rng = np.random.default_rng(5)
-    f, k = 8192, 2048
+    rng = np.random.default_rng(5 + f + k)
     wq, ws = _int4(rng, 2 * f, k)
     x = rng.standard_normal(k).astype(np.float32)
     nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float16)

@@ -86,11 +86,11 @@ def test_add_residual(dev, tokens, k):
     assert rel_inf(to_np(y), ref) < TOL_FP32
 
 
-@pytest.mark.parametrize("tokens", [1, 3])
-def test_gate_up(dev, tokens):
+@pytest.mark.parametrize("tokens,f", [(1, 768), (3, 768), (1, 8192), (1, 4096 + 16 + 7)])
+def test_gate_up(dev, tokens, f):
     import torch
-    rng = np.random.default_rng(11)
-    f, k, g = 768, 2048, 32
+    rng = np.random.default_rng(11 + f)
+    k, g = 2048, 32
     wq = rng.integers(0, 2 ** 32, (2 * f, k // 8), dtype=np.uint32)
     ws = (np.abs(rng.standard_normal((2 * f, k // g))) * 0.02 + 1e-3).astype(np.float16)
     x = rng.standard_normal((tokens, k)).astype(np.float32)
