@@ -118,8 +118,17 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
   for (int i = threadIdx.x; i < E * W; i += 1024) bits[i] = 0ull;
   for (int r = threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;  // padding rows; real rows are set below
   __syncthreads();
+  // this thread's first kIdReg ids stay in registers for the placement below (a second read would wait on memory)
+  constexpr int kIdReg = 4;
+  int idr[kIdReg];
+#pragma unroll
+  for (int q = 0; q < kIdReg; ++q) {
+    const int i = threadIdx.x + 1024 * q;
+    idr[q] = i < n ? ids[i] : -1;
+  }
   for (int i = threadIdx.x; i < n; i += 1024) {
-    const int e = ids[i];
+    const int q = i >> 10;
+    const int e = q < kIdReg ? idr[q < kIdReg ? q : 0] : ids[i];
     if (e >= 0 && e < E) {
       const unsigned long long bit = 1ull << ((i / topk) & 63);
       if (atomicOr(&bits[(size_t)e * W + ((i / topk) >> 6)], bit) & bit) repeated = 1;
@@ -210,7 +219,8 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
     if (o.lists && rank < o.cap) o.lists[(size_t)ex * o.cap + rank] = i;
   };
   for (int i = threadIdx.x; i < n; i += 1024) {
-    const int ex = ids[i];
+    const int q = i >> 10;
+    const int ex = q < kIdReg ? idr[q < kIdReg ? q : 0] : ids[i];
     if (ex < 0 || ex >= E) {
       o.slot[i] = -1;  // an id outside [0, E) is in no group
       continue;
@@ -227,6 +237,9 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
 }
 
 // ---- combine: y[t, c] = (add ? y[t, c] : 0) + sum_k w[t, k] * yd[slot[t*topk + k], c], k in order ----
+// KT: a compile-time bound on topk (0: any topk, one entry at a time). With KT, every entry's slot and weight and then
+// every row's 16 bytes are requested before the first is used, so the eight row reads are in flight together.
+template <int KT>
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ yd, const int32_t* __restrict__ slot,
                                                      const float* __restrict__ w, float* __restrict__ y, int tokens,
                                                      int d, int topk, int add, int yd_rows) {
@@ -236,15 +249,38 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
     const int t = (int)(i / d4);
     const int c = (int)(i - (int64_t)t * d4);
     float4 acc = add ? reinterpret_cast<const float4*>(y + (size_t)t * d)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < topk; ++k) {
-      const int r = slot ? slot[t * topk + k] : t * topk + k;
-      if (r < 0 || r >= yd_rows) continue;  // an entry in no group contributes nothing
-      const float wk = w[t * topk + k];
-      const float4 v = reinterpret_cast<const float4*>(yd + (size_t)r * d)[c];
-      acc.x = fmaf(wk, v.x, acc.x);
-      acc.y = fmaf(wk, v.y, acc.y);
-      acc.z = fmaf(wk, v.z, acc.z);
-      acc.w = fmaf(wk, v.w, acc.w);
+    if constexpr (KT > 0) {
+      int r[KT];
+      float wk[KT];
+#pragma unroll
+      for (int k = 0; k < KT; ++k) {
+        const int rr = k < topk ? (slot ? slot[t * topk + k] : t * topk + k) : -1;
+        r[k] = (rr >= 0 && rr < yd_rows) ? rr : -1;  // an entry in no group contributes nothing
+        wk[k] = k < topk ? w[t * topk + k] : 0.f;
+      }
+      float4 v[KT];
+#pragma unroll
+      for (int k = 0; k < KT; ++k)
+        v[k] = r[k] >= 0 ? reinterpret_cast<const float4*>(yd + (size_t)r[k] * d)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < KT; ++k) {
+        if (r[k] < 0) continue;  // as in the loop below: a skipped entry adds nothing (not even 0 * NaN)
+        acc.x = fmaf(wk[k], v[k].x, acc.x);
+        acc.y = fmaf(wk[k], v[k].y, acc.y);
+        acc.z = fmaf(wk[k], v[k].z, acc.z);
+        acc.w = fmaf(wk[k], v[k].w, acc.w);
+      }
+    } else {
+      for (int k = 0; k < topk; ++k) {
+        const int r = slot ? slot[t * topk + k] : t * topk + k;
+        if (r < 0 || r >= yd_rows) continue;  // an entry in no group contributes nothing
+        const float wk = w[t * topk + k];
+        const float4 v = reinterpret_cast<const float4*>(yd + (size_t)r * d)[c];
+        acc.x = fmaf(wk, v.x, acc.x);
+        acc.y = fmaf(wk, v.y, acc.y);
+        acc.z = fmaf(wk, v.z, acc.z);
+        acc.w = fmaf(wk, v.w, acc.w);
+      }
     }
     reinterpret_cast<float4*>(y + (size_t)t * d)[c] = acc;
   }
@@ -389,8 +425,12 @@ extern "C" int aq_moe_combine(const float* yd, int64_t yd_rows, const int32_t* s
   if (!aligned(yd, 16) || !aligned(y, 16)) return AQ_ERR_ALIGN;
   int64_t blocks = (tokens * d / 4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), yd,
-                     slot, weights, y, (int)tokens, (int)d, topk, add, (int)yd_rows);
+  if (topk <= 8)
+    hipLaunchKernelGGL(k_moe_combine<8>, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       yd, slot, weights, y, (int)tokens, (int)d, topk, add, (int)yd_rows);
+  else
+    hipLaunchKernelGGL(k_moe_combine<0>, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       yd, slot, weights, y, (int)tokens, (int)d, topk, add, (int)yd_rows);
   return launch_status();
 }
 
