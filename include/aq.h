@@ -260,14 +260,16 @@ int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const float* parts, i
 
 /* Final norm, lm_head and greedy argmax: logits = W . rmsnorm(x) (norm_w NULL: x as given), then *token = the first
  * index of the largest logit, hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance.
- * One launch: every workgroup leaves its best argmax key in cand and counts itself on the 32-bit word at the start of
- * cand's last slot; the workgroup that arrives last writes the token and sets that word back to zero.
+ * One launch: every workgroup (at most 1024) leaves its best argmax key in cand and counts itself on arrival
+ * counters kept in cand's last AQ_HEAD_ARRIVAL_SLOTS slots; the workgroup that arrives last writes the token and sets
+ * the counters back to zero.
  * cand: device scratch of cand_cap 8-byte slots (8-byte aligned; AQ_HEAD_CANDIDATES is enough for any vocab), whose
- * last slot must be zero before the first call (a zero-filled buffer) and is left zero by every call; calls sharing
- * a cand must be ordered on one stream. NaN logits never win, as in the reference's `logits[i] > logits[best]` scan
+ * last AQ_HEAD_ARRIVAL_SLOTS slots must be zero before the first call (a zero-filled buffer) and are left zero by
+ * every call; calls sharing a cand must be ordered on one stream. NaN logits never win, as in the reference's `logits[i] > logits[best]` scan
  * (which differs only when logit 0 itself is NaN: it then returns 0).
  * Replaces: Llama.head (llama/model.mojo:160-166) and the host argmax scan (llama/llama.mojo:72-75). */
 #define AQ_HEAD_CANDIDATES 4096
+#define AQ_HEAD_ARRIVAL_SLOTS 17
 int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w, float eps,
                       float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand, int64_t cand_cap,
                       int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap, int32_t advance, void* stream);

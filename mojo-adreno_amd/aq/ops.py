@@ -461,8 +461,9 @@ for _name, _fn in (("moe_route", _moe_route_impl), ("moe_route_pack", _moe_route
 
 # ---- Llama decode step: fused norms, embedding, attention, lm_head + argmax -----------------------------------------
 
-HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax key slots of a head launch (the int4 head keeps its arrival counter
-#                         in the last one: allocate zero-filled)
+HEAD_CANDIDATES = 4096  # AQ_HEAD_CANDIDATES: argmax key slots of a head launch (the int4 head keeps its arrival
+#                         counters in the last HEAD_ARRIVAL_SLOTS: allocate zero-filled)
+HEAD_ARRIVAL_SLOTS = 17  # AQ_HEAD_ARRIVAL_SLOTS
 ATTN_MAX_SPLITS = 8     # AQ_ATTN_MAX_SPLITS
 
 

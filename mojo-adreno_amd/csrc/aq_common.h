@@ -117,14 +117,26 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)idx;
 }
-// Maximum of a 64-bit value over the wave, in every lane.
+// m = max(m, the 64-bit value DPP brings from another lane), both halves moved by the same DPP control
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t m) {
+  const uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > m ? o : m;
+}
+// Maximum of a 64-bit value over the wave, in every lane (the steps of wave_max, read back from lane 63).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    const uint64_t o = __shfl_xor(m, s, kWave);
-    m = o > m ? o : m;
-  }
-  return m;
+  m = dpp_max_u64<0xB1, 0xF>(m);
+  m = dpp_max_u64<0x4E, 0xF>(m);
+  m = dpp_max_u64<0x141, 0xF>(m);
+  m = dpp_max_u64<0x140, 0xF>(m);
+  m = dpp_max_u64<0x142, 0xA>(m);
+  m = dpp_max_u64<0x143, 0xC>(m);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)m, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(m >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 // The key a producer leaves when any of its values is not finite: above every key of a finite value, so the step's

@@ -35,9 +35,12 @@ struct MoeArgs {
 // parts != NULL (one token): x is the attention output combined from `splits` partial softmax states (the layout of
 // aq_attn_decode_split): x[h * 64 + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
 // cand != NULL also ends the greedy step in the same launch: each workgroup leaves its best key in cand[block] and
-// counts itself on `arrivals`; the one that arrives last (every other key is then stored) takes the largest key and
-// writes *token, hist[*pos] and *pos += advance, then sets the counter back to zero. The keys are stored and read
-// with device-coherent (sc1) accesses and the counter is a device-scope atomic, so no cache writeback is needed.
+// counts itself; the one that arrives last (every other key is then stored) takes the largest key and writes *token,
+// hist[*pos] and *pos += advance. The count is two-level, so that no counter takes more than ~64 of the launch's
+// atomics at once: workgroup b counts on the counter of group b % 16, and the group's last member counts on the top
+// counter and sets its group's back to zero; the last on the top counter sets that one back to zero. The keys are
+// stored and read with device-coherent (sc1) accesses and the counters are device-scope atomics, so no cache
+// writeback is needed.
 struct Fuse {
   const uint16_t* norm;
   float eps;
@@ -50,8 +53,10 @@ struct Fuse {
   int32_t* hist;
   int hist_cap;
   int advance;
-  uint32_t* arrivals;
+  uint32_t* arrivals;  // AQ_HEAD_ARRIVAL_SLOTS 8-byte slots: the top counter in slot 0, group g's in slot g + 1
 };
+constexpr int kArrivalGroups = AQ_HEAD_ARRIVAL_SLOTS - 1;
+constexpr int kMaxHeadBlocks = 1024;  // gemv_blocks' cap: the last workgroup reads this many keys at most
 
 
 // Weight row r of the output block starting at `base` (every mode but kMoeDown; -1 = no row, kMoeGateUp only). Rows
@@ -496,38 +501,47 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   if constexpr (MODE == kStore) {
     if (fz.cand) {  // workgroup-uniform
       __shared__ uint64_t wkey[4];
-      __shared__ int last;
       if (lane == 0) wkey[wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
       __syncthreads();
-      const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(fz.cand, gridDim.x * 8u);
-      if (threadIdx.x == 0) {
-        uint64_t m = wkey[0];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) m = wkey[w] > m ? wkey[w] : m;
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, m), c_rsrc, blockIdx.x * 8u, 0, kSc1);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the key has reached device scope
-        last = __hip_atomic_fetch_add(fz.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-      }
-      __syncthreads();
-      if (last) {  // workgroup-uniform: every workgroup's key is stored
-        uint64_t m = 0;
-        for (uint32_t i = threadIdx.x; i < gridDim.x; i += 256) {
-          const uint64_t c = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(c_rsrc, i * 8u, 0, kSc1));
-          m = c > m ? c : m;
-        }
-        m = wave_max_u64(m);
-        if (lane == 0) wkey[wave] = m;
-        __syncthreads();
-        if (threadIdx.x == 0) {
+      if (wave == 0) {  // the rest of the step is wave 0's
+        const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(fz.cand, gridDim.x * 8u);
+        uint32_t last = 0;
+        if (lane == 0) {
+          uint64_t m = wkey[0];
 #pragma unroll
           for (int w = 1; w < 4; ++w) m = wkey[w] > m ? wkey[w] : m;
-          const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
-          const int p = *fz.pos;
-          *fz.token = idx;
-          if (fz.hist && p >= 0 && p < fz.hist_cap) fz.hist[p] = idx;
-          *fz.pos = p + fz.advance;
-          __hip_atomic_store(fz.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, m), c_rsrc, blockIdx.x * 8u, 0, kSc1);
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the key has reached device scope
+          // two-level count: workgroup b counts on group b % ng's counter; the group's last counts on the top one
+          const uint32_t ng = gridDim.x < kArrivalGroups ? gridDim.x : kArrivalGroups, g = blockIdx.x % ng;
+          const uint32_t members = (gridDim.x - g + ng - 1) / ng;
+          uint32_t* gc = fz.arrivals + 2 * (g + 1);
+          if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1) {
+            __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // every member has counted
+            last = __hip_atomic_fetch_add(fz.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1;
+          }
+        }
+        if (__builtin_amdgcn_readfirstlane(last)) {  // every workgroup's key is stored
+          uint64_t kv[kMaxHeadBlocks / kWave];
+#pragma unroll
+          for (int i = 0; i < kMaxHeadBlocks / kWave; ++i) {
+            const uint32_t b = lane + kWave * i;
+            kv[i] = __builtin_bit_cast(uint64_t,
+                                       __builtin_amdgcn_raw_buffer_load_b64(c_rsrc, b < gridDim.x ? b * 8u : kOOB, 0, kSc1));
+          }
+          uint64_t m = kv[0];
+#pragma unroll
+          for (int i = 1; i < kMaxHeadBlocks / kWave; ++i) m = kv[i] > m ? kv[i] : m;
+          m = wave_max_u64(m);
+          if (lane == 0) {
+            const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
+            const int p = *fz.pos;
+            *fz.token = idx;
+            if (fz.hist && p >= 0 && p < fz.hist_cap) fz.hist[p] = idx;
+            *fz.pos = p + fz.advance;
+            __hip_atomic_store(fz.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
       }
     }
@@ -729,7 +743,7 @@ static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, flo
 // Workgroups of a launch over n_out outputs, RO per wave: one pass of 4 waves each, at most 1024 (then grid-stride).
 inline int gemv_blocks(int64_t n_out, int ro) {
   const int64_t b = (n_out + 4 * ro - 1) / (4 * ro);
-  return b > 1024 ? 1024 : (int)b;
+  return b > kMaxHeadBlocks ? kMaxHeadBlocks : (int)b;
 }
 
 template <bool G32, int R, int T, int MODE, int D, int XR>
@@ -942,9 +956,9 @@ extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const f
                                  int32_t advance, void* stream) {
   if (!cand || !token || !pos) return AQ_ERR_NULL;
   if (vocab <= 0 || vocab > (int64_t)1 << 30 || hist_cap < 0) return AQ_ERR_SHAPE;
-  // one key per workgroup, and the arrival counter in the last slot
+  // one key per workgroup, and the arrival counters in the last AQ_HEAD_ARRIVAL_SLOTS slots
   const int ncand = aq::gemv_blocks(vocab, aq::rows_per_wave(vocab));
-  if (cand_cap < ncand + 1) return AQ_ERR_CAPACITY;
+  if (cand_cap < ncand + AQ_HEAD_ARRIVAL_SLOTS) return AQ_ERR_CAPACITY;
   if (!aq::aligned(cand, 8)) return AQ_ERR_ALIGN;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
   aq::Fuse fz{norm_w, eps, cand, nullptr, 0};
@@ -953,7 +967,7 @@ extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const f
   fz.hist = hist;
   fz.hist_cap = hist_cap;
   fz.advance = advance;
-  fz.arrivals = reinterpret_cast<uint32_t*>(cand + (cand_cap - 1));
+  fz.arrivals = reinterpret_cast<uint32_t*>(cand + (cand_cap - AQ_HEAD_ARRIVAL_SLOTS));
   return aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream, fz);
 }
 

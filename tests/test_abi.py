@@ -28,6 +28,15 @@ def test_bindings_cover_every_declared_symbol():
     assert names <= set(_lib.SIGNATURES), f"no ctypes signature for {sorted(names - set(_lib.SIGNATURES))}"
 
 
+def test_python_constants_match_the_header():
+    """The limits aq.ops mirrors are the header's #defines."""
+    from aq import ops
+    text = (ROOT / "include" / "aq.h").read_text()
+    defs = dict(re.findall(r"^#define AQ_(\w+) (\d+)\s*$", text, flags=re.M))
+    for name in ("HEAD_CANDIDATES", "HEAD_ARRIVAL_SLOTS", "ATTN_MAX_SPLITS", "STREAM_READ_MAX_BLOCKS"):
+        assert int(defs[name]) == getattr(ops, name), name
+
+
 def test_status_strings():
     from aq import _lib
     assert _lib.status_string(0) == "ok"
@@ -97,8 +106,10 @@ def test_decode_entries_reject_bad_arguments_before_launch():
     assert lib.aq_attn_decode(p, p, p, p, p, p, 48, 3, 64, 512, p, None) == 1           # 16 heads per KV head
     assert lib.aq_attn_decode(p, p, p, p, p, p, 32, 4, 64, 8192, p, None) == 6          # scores exceed LDS
     assert lib.aq_attn_decode(p, p, p, None, p, p, 32, 8, 64, 512, p, None) == 5
-    # lm_head: 128256 rows need 4 * 1024 argmax candidates; the position pointer is required
+    # lm_head: 128256 rows take 1024 workgroups, so 1024 argmax keys and the arrival counters' 17 slots; the position
+    # pointer is required
     assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 128256, 2048, 32, p, 1000, p, p, None, 0, 1, None) == 6
+    assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 128256, 2048, 32, p, 1024 + 16, p, p, None, 0, 1, None) == 6
     assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 1000, 2048, 32, p, 4096, p, None, None, 0, 1, None) == 5
     assert lib.aq_head_argmax_q4(p, p, p, None, f, p, 1000, 2048, 32, p + 4, 4096, p, p, None, 0, 1, None) == 3
 

@@ -136,13 +136,16 @@ def test_head_argmax(dev, vocab):
     assert h[5] == best and (np.delete(h, 5) == -1).all()
 
 
-def test_head_argmax_one_launch_repeats(dev):
-    """The head ends the greedy step in its own launch (the last workgroup to arrive picks the token): the arrival
-    counter in cand's last slot is back at zero after every call, so calls in a row, eager and replayed from one
-    graph, each give the oracle's token and advance the position."""
+@pytest.mark.parametrize("vocab", [37, 1000, 50000])
+def test_head_argmax_one_launch_repeats(dev, vocab):
+    """The head ends the greedy step in its own launch (the last workgroup to arrive picks the token, counted on a
+    two-level set of arrival counters): the counters in cand's last HEAD_ARRIVAL_SLOTS slots are back at zero after
+    every call, so calls in a row, eager and replayed from one graph, each give the oracle's token and advance the
+    position. 37, 1000 and 50000 rows take 5 workgroups (one per counter group), 63 (groups of 3 and 4) and 1024."""
     import torch
+    from aq import ops
     rng = np.random.default_rng(77)
-    vocab, k = 50000, 2048
+    k = 2048
     wq, ws = _int4(rng, vocab, k)
     xs = [rng.standard_normal(k).astype(np.float32) for _ in range(3)]
     logits = torch.empty(vocab, dtype=torch.float32, device=dev)
@@ -159,7 +162,7 @@ def test_head_argmax_one_launch_repeats(dev):
         x.copy_(to_dev(xv, dev))
         run()
         assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
-        assert int(to_np(cand)[-1]) == 0
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         run()
@@ -169,7 +172,7 @@ def test_head_argmax_one_launch_repeats(dev):
         g.replay()
         torch.cuda.synchronize()
         assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
-        assert int(to_np(cand)[-1]) == 0
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
     np.testing.assert_array_equal(to_np(hist)[:3], np.array(want, np.int32))
 
 
