@@ -175,10 +175,12 @@ int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float*
                void* workspace, int64_t workspace_bytes, void* stream);
 int64_t aq_t2_gemv_workspace_bytes(int64_t n, int64_t k);
 
-/* Ternary output head with greedy argmax on the device: logits = the aq_t2_gemv product over the vocabulary rows,
- * each workgroup also leaving the argmax key of its columns in cand (aq_t2_head_candidates(n, k) of them, 8-byte
- * aligned); then *token = the first index of the largest logit, or -1 when any logit is NaN or infinite,
- * hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance. Replaces: packed_head with
+/* Ternary output head with greedy argmax on the device, one launch: logits = the aq_t2_gemv product over the
+ * vocabulary rows, then *token = the first index of the largest logit, or -1 when any logit is NaN or infinite,
+ * hist[*pos] = *token when 0 <= *pos < hist_cap (hist may be NULL), *pos += advance. cand: aq_t2_head_candidates(n, k)
+ * 8-byte slots (8-byte aligned): an argmax key per workgroup, then the arrival counters in the last
+ * AQ_HEAD_ARRIVAL_SLOTS slots, as in aq_head_argmax_q4 (zero before the first call, left zero; calls sharing a cand
+ * ordered on one stream). Replaces: packed_head with
  * select = 1 (bonsai/kernels/kernels.mojo:451-517: logits plus per-64-lane (best, index, nonfinite) candidates) and
  * the host's greedy() over them (bonsai/bonsai_vk.c:506-515: largest value, lowest index on ties; a nonfinite flag
  * stops it with "nonfinite logits"). */
@@ -282,10 +284,11 @@ int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, co
 int aq_gemv_q6(const uint8_t* q, const uint16_t* d, const float* x, float* y, int64_t rows, int64_t cols,
                void* stream);
 
-/* Final norm, Q6_K head and greedy argmax: logits = E . rmsnorm(x) (norm_w NULL: x as given), then as
+/* Final norm, Q6_K head and greedy argmax, one launch: logits = E . rmsnorm(x) (norm_w NULL: x as given), then as
  * aq_head_argmax_q4: *token = the first index of the largest logit (NaN never wins), hist[*pos] = *token when
- * 0 <= *pos < hist_cap, *pos += advance. cand: aq_head_q6_candidates(rows, cols) <= AQ_HEAD_CANDIDATES argmax keys,
- * 8-byte aligned. Replaces: head_q6 + argmax (lfm2/kernels/lk.mojo:179-221: lowest index among equal maxima). */
+ * 0 <= *pos < hist_cap, *pos += advance. cand: aq_head_q6_candidates(rows, cols) <= AQ_HEAD_CANDIDATES 8-byte slots
+ * (8-byte aligned): an argmax key per workgroup, then the arrival counters in the last AQ_HEAD_ARRIVAL_SLOTS slots,
+ * as in aq_head_argmax_q4 (zero before the first call, left zero; calls sharing a cand ordered on one stream). Replaces: head_q6 + argmax (lfm2/kernels/lk.mojo:179-221: lowest index among equal maxima). */
 int aq_head_argmax_q6(const uint8_t* q, const uint16_t* d, const float* x, const uint16_t* norm_w, float eps,
                       float* logits, int64_t rows, int64_t cols, uint64_t* cand, int64_t cand_cap, int32_t* token,
                       int32_t* pos, int32_t* hist, int32_t hist_cap, int32_t advance, void* stream);

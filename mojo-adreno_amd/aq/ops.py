@@ -169,7 +169,8 @@ def _t2_gemv_impl(x2h, w, s, y, workspace):
 
 
 def t2_head_candidates(n: int, k: int) -> int:
-    """Argmax keys the ternary head leaves for an N x K head (one per workgroup)."""
+    """8-byte slots of the ternary head's cand for an N x K head: an argmax key per workgroup, then the arrival
+    counters (HEAD_ARRIVAL_SLOTS). Allocate zero-filled."""
     return int(_lib.lib().aq_t2_head_candidates(n, k))
 
 
@@ -599,7 +600,8 @@ _LIB.define("embed_q6(Tensor q, Tensor d, Tensor ids, Tensor(a!) x) -> ()")
 
 
 def head_q6_candidates(rows: int, cols: int) -> int:
-    """Argmax keys the Q6_K head leaves (one per wave, at most HEAD_CANDIDATES)."""
+    """8-byte slots of the Q6_K head's cand: an argmax key per workgroup, then the arrival counters (at most
+    HEAD_CANDIDATES). Allocate zero-filled."""
     return int(_lib.lib().aq_head_q6_candidates(rows, cols))
 
 

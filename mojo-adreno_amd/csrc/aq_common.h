@@ -143,11 +143,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
 // maximum is this key exactly when some logit was NaN or infinite (the token is then -1).
 constexpr uint64_t kNonFiniteKey = ~0ull;
 
-// Greedy-decode step end (aq_gemv.hip): the largest of ncand argmax keys becomes *token (and hist[*pos]), -1 when
-// that is kNonFiniteKey, then *pos += advance. One workgroup.
-int launch_argmax_step(const uint64_t* cand, int ncand, int32_t* token, int32_t* pos, int32_t* hist, int hist_cap,
-                       int advance, hipStream_t s);
-
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 inline int launch_status() {

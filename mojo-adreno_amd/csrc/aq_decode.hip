@@ -8,7 +8,7 @@
 // values are rounded once, when stored, and every read (this position's too) sees the stored fp16 values.
 //
 // Positions come from device memory (*pos), so a captured step can be replayed while the position advances on the
-// device (see k_argmax_step).
+// device (the head's launch advances it: aq_step_end.h).
 #include "aq_common.h"
 
 namespace aq {

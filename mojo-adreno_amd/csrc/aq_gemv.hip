@@ -13,6 +13,7 @@
 // v_cvt_f32_ubyte) against fp32 x and subtract 8 * sum(x) once per chunk. Row sums end in a wave reduction.
 #include "aq_common.h"
 #include "aq_digits.h"
+#include "aq_step_end.h"
 #include "aq_moe_decode.h"
 
 namespace aq {
@@ -30,33 +31,17 @@ struct MoeArgs {
 };
 
 // Decode-step fusions. norm != NULL: every token's x is RMS-normalised on staging, x * (1 / sqrt(mean(x^2) + eps))
-// * norm[k] (fp16 weights), so no separate norm kernel runs before the product. cand != NULL (kStore, one token):
-// each wave also leaves the largest output it wrote and its row, as an argmax key (cand[block * 4 + wave]).
+// * norm[k] (fp16 weights), so no separate norm kernel runs before the product.
 // parts != NULL (one token): x is the attention output combined from `splits` partial softmax states (the layout of
 // aq_attn_decode_split): x[h * 64 + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
-// cand != NULL also ends the greedy step in the same launch: each workgroup leaves its best key in cand[block] and
-// counts itself; the one that arrives last (every other key is then stored) takes the largest key and writes *token,
-// hist[*pos] and *pos += advance. The count is two-level, so that no counter takes more than ~64 of the launch's
-// atomics at once: workgroup b counts on the counter of group b % 16, and the group's last member counts on the top
-// counter and sets its group's back to zero; the last on the top counter sets that one back to zero. The keys are
-// stored and read with device-coherent (sc1) accesses and the counters are device-scope atomics, so no cache
-// writeback is needed.
+// With step.cand the launch also ends the greedy step (step_end): each workgroup's best key, then the token.
 struct Fuse {
   const uint16_t* norm;
   float eps;
-  uint64_t* cand;
   const float* parts;
   int splits;
-  // with cand: the greedy step's outputs, and the arrival counter (a 32-bit word, zero between launches)
-  int32_t* token;
-  int32_t* pos;
-  int32_t* hist;
-  int hist_cap;
-  int advance;
-  uint32_t* arrivals;  // AQ_HEAD_ARRIVAL_SLOTS 8-byte slots: the top counter in slot 0, group g's in slot g + 1
+  StepEnd step;  // kStore, one token (step.cand NULL: none)
 };
-constexpr int kArrivalGroups = AQ_HEAD_ARRIVAL_SLOTS - 1;
-constexpr int kMaxHeadBlocks = 1024;  // gemv_blocks' cap: the last workgroup reads this many keys at most
 
 
 // Weight row r of the output block starting at `base` (every mode but kMoeDown; -1 = no row, kMoeGateUp only). Rows
@@ -499,52 +484,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
     finish(base, acc);
   }
   if constexpr (MODE == kStore) {
-    if (fz.cand) {  // workgroup-uniform
-      __shared__ uint64_t wkey[4];
-      if (lane == 0) wkey[wave] = best_row < 0 ? 0ull : argmax_key(best, best_row);
-      __syncthreads();
-      if (wave == 0) {  // the rest of the step is wave 0's
-        const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(fz.cand, gridDim.x * 8u);
-        uint32_t last = 0;
-        if (lane == 0) {
-          uint64_t m = wkey[0];
-#pragma unroll
-          for (int w = 1; w < 4; ++w) m = wkey[w] > m ? wkey[w] : m;
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, m), c_rsrc, blockIdx.x * 8u, 0, kSc1);
-          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the key has reached device scope
-          // two-level count: workgroup b counts on group b % ng's counter; the group's last counts on the top one
-          const uint32_t ng = gridDim.x < kArrivalGroups ? gridDim.x : kArrivalGroups, g = blockIdx.x % ng;
-          const uint32_t members = (gridDim.x - g + ng - 1) / ng;
-          uint32_t* gc = fz.arrivals + 2 * (g + 1);
-          if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1) {
-            __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // every member has counted
-            last = __hip_atomic_fetch_add(fz.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1;
-          }
-        }
-        if (__builtin_amdgcn_readfirstlane(last)) {  // every workgroup's key is stored
-          uint64_t kv[kMaxHeadBlocks / kWave];
-#pragma unroll
-          for (int i = 0; i < kMaxHeadBlocks / kWave; ++i) {
-            const uint32_t b = lane + kWave * i;
-            kv[i] = __builtin_bit_cast(uint64_t,
-                                       __builtin_amdgcn_raw_buffer_load_b64(c_rsrc, b < gridDim.x ? b * 8u : kOOB, 0, kSc1));
-          }
-          uint64_t m = kv[0];
-#pragma unroll
-          for (int i = 1; i < kMaxHeadBlocks / kWave; ++i) m = kv[i] > m ? kv[i] : m;
-          m = wave_max_u64(m);
-          if (lane == 0) {
-            const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
-            const int p = *fz.pos;
-            *fz.token = idx;
-            if (fz.hist && p >= 0 && p < fz.hist_cap) fz.hist[p] = idx;
-            *fz.pos = p + fz.advance;
-            __hip_atomic_store(fz.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-    }
+    // workgroup-uniform; lane 0 holds its wave's first maximum (rows arrive in ascending order)
+    if (fz.step.cand) workgroup_step_end<4>(fz.step, best_row < 0 ? 0ull : argmax_key(best, best_row));
   }
 }
 
@@ -743,7 +684,7 @@ static int launch_ks(const uint32_t* wq, const uint16_t* ws, const float* x, flo
 // Workgroups of a launch over n_out outputs, RO per wave: one pass of 4 waves each, at most 1024 (then grid-stride).
 inline int gemv_blocks(int64_t n_out, int ro) {
   const int64_t b = (n_out + 4 * ro - 1) / (4 * ro);
-  return b > kMaxHeadBlocks ? kMaxHeadBlocks : (int)b;
+  return b > 1024 ? 1024 : (int)b;
 }
 
 template <bool G32, int R, int T, int MODE, int D, int XR>
@@ -825,7 +766,7 @@ static int launch_g(const uint32_t* wq, const uint16_t* ws, const float* x, floa
 template <int MODE>
 static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, float* y, int64_t n_out, int64_t k,
                       int32_t group, int64_t f, int32_t tokens, const MoeArgs& moe, void* stream,
-                      const Fuse& fz = Fuse{nullptr, 0.f, nullptr, nullptr, 0}) {
+                      const Fuse& fz = Fuse{nullptr, 0.f, nullptr, 0, {}}) {
   if (!wq || !ws || !x || !y) return AQ_ERR_NULL;
   if (fz.norm && !aligned(fz.norm, 16)) return AQ_ERR_ALIGN;
   const int max_tokens = (MODE == kStore || MODE == kAdd) ? 16 : 8;
@@ -842,7 +783,7 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool g32 = group >= 32 && (group & (group - 1)) == 0;
   if constexpr (MODE == kStore || MODE == kAdd || MODE == kGateUp) {
-    if (g32 && tokens == 1 && !fz.cand && !fz.parts) {
+    if (g32 && tokens == 1 && !fz.step.cand && !fz.parts) {
       const int ks = gemv_k_slices(n_out, k, MODE == kGateUp);
       const int fi = (int)f;
       if (ks == 1) return launch_ks<1, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, fi, fz.norm, fz.eps, s);
@@ -853,40 +794,6 @@ static int gemv_entry(const uint32_t* wq, const uint16_t* ws, const float* x, fl
   if (g32)
     return launch_g<true, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
   return launch_g<false, MODE>(wq, ws, x, y, (int)n_out, (int)k, group, (int)f, tokens, moe, fz, s);
-}
-
-// Greedy-decode step end: the maximum of ncand argmax keys names the next token; it is written to *token and to
-// hist[*pos] (when hist_cap > *pos), then *pos advances by `advance`. One workgroup.
-__global__ __launch_bounds__(1024) void k_argmax_step(const uint64_t* __restrict__ cand, int ncand,
-                                                      int32_t* __restrict__ token, int32_t* __restrict__ pos,
-                                                      int32_t* __restrict__ hist, int hist_cap, int advance) {
-  __shared__ uint64_t red[16];
-  uint64_t m = 0;
-  for (int i = threadIdx.x; i < ncand; i += 1024) {
-    const uint64_t c = cand[i];
-    m = c > m ? c : m;
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint64_t o = __shfl_xor(m, d, kWave);
-    m = o > m ? o : m;
-  }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 16; ++w) m = red[w] > m ? red[w] : m;  // m is red[0] here
-    const int idx = m == kNonFiniteKey ? -1 : m ? (int)~(uint32_t)m : 0;
-    const int p = *pos;
-    *token = idx;
-    if (hist && p >= 0 && p < hist_cap) hist[p] = idx;
-    *pos = p + advance;
-  }
-}
-
-int launch_argmax_step(const uint64_t* cand, int ncand, int32_t* token, int32_t* pos, int32_t* hist, int hist_cap,
-                       int advance, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, cand, ncand, token, pos, hist, hist_cap, advance);
-  return launch_status();
 }
 
 }  // namespace aq
@@ -938,7 +845,7 @@ extern "C" int aq_rmsnorm_gemv_q4(const uint32_t* wq, const uint16_t* ws, const 
                                   void* stream) {
   if (!norm_w) return AQ_ERR_NULL;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
-  return aq::gemv_entry<aq::kStore>(wq, ws, x, y, n, k, group, 0, tokens, none, stream, aq::Fuse{norm_w, eps, nullptr, nullptr, 0});
+  return aq::gemv_entry<aq::kStore>(wq, ws, x, y, n, k, group, 0, tokens, none, stream, aq::Fuse{norm_w, eps, nullptr, 0, {}});
 }
 
 extern "C" int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
@@ -947,27 +854,20 @@ extern "C" int aq_rmsnorm_gate_up_q4(const uint32_t* wq, const uint16_t* ws, con
   if (!norm_w) return AQ_ERR_NULL;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
   return aq::gemv_entry<aq::kGateUp>(wq, ws, x, a, f, k, group, f, tokens, none, stream,
-                                     aq::Fuse{norm_w, eps, nullptr, nullptr, 0});
+                                     aq::Fuse{norm_w, eps, nullptr, 0, {}});
 }
 
 extern "C" int aq_head_argmax_q4(const uint32_t* wq, const uint16_t* ws, const float* x, const uint16_t* norm_w,
                                  float eps, float* logits, int64_t vocab, int64_t k, int32_t group, uint64_t* cand,
                                  int64_t cand_cap, int32_t* token, int32_t* pos, int32_t* hist, int32_t hist_cap,
                                  int32_t advance, void* stream) {
-  if (!cand || !token || !pos) return AQ_ERR_NULL;
-  if (vocab <= 0 || vocab > (int64_t)1 << 30 || hist_cap < 0) return AQ_ERR_SHAPE;
-  // one key per workgroup, and the arrival counters in the last AQ_HEAD_ARRIVAL_SLOTS slots
-  const int ncand = aq::gemv_blocks(vocab, aq::rows_per_wave(vocab));
-  if (cand_cap < ncand + AQ_HEAD_ARRIVAL_SLOTS) return AQ_ERR_CAPACITY;
-  if (!aq::aligned(cand, 8)) return AQ_ERR_ALIGN;
+  if (vocab <= 0 || vocab > (int64_t)1 << 30) return AQ_ERR_SHAPE;
+  // one key per workgroup, then the arrival counters
+  aq::Fuse fz{norm_w, eps, nullptr, 0, {}};
+  const int st = aq::make_step_end(cand, cand_cap, aq::gemv_blocks(vocab, aq::rows_per_wave(vocab)), token, pos, hist,
+                                   hist_cap, advance, fz.step);
+  if (st != AQ_OK) return st;
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
-  aq::Fuse fz{norm_w, eps, cand, nullptr, 0};
-  fz.token = token;
-  fz.pos = pos;
-  fz.hist = hist;
-  fz.hist_cap = hist_cap;
-  fz.advance = advance;
-  fz.arrivals = reinterpret_cast<uint32_t*>(cand + (cand_cap - AQ_HEAD_ARRIVAL_SLOTS));
   return aq::gemv_entry<aq::kStore>(wq, ws, x, logits, vocab, k, group, 0, 1, none, stream, fz);
 }
 
@@ -979,5 +879,5 @@ extern "C" int aq_attn_out_q4(const uint32_t* wq, const uint16_t* ws, const floa
   const aq::MoeArgs none{nullptr, nullptr, 0, 0};
   // x is not read (the partial states stand for it); parts is passed as x for the pointer checks
   return aq::gemv_entry<aq::kAdd>(wq, ws, parts, y, n, k, group, 0, 1, none, stream,
-                                  aq::Fuse{nullptr, 0.f, nullptr, parts, splits});
+                                  aq::Fuse{nullptr, 0.f, parts, splits, {}});
 }

@@ -14,13 +14,14 @@
 // Replaces: head_q6 / q6_chunk (lfm2/kernels/lk.mojo:88-129,179-191), the device argmax after it (:194-221) and
 // embed_q6 (:224-232).
 #include "aq_common.h"
+#include "aq_step_end.h"
 
 namespace aq {
 namespace {
 
 constexpr int kQ6Bytes = 208;   // bytes of a super-block in q
 constexpr int kQ6Waves = 3072;  // waves of a head launch at most: 3 a SIMD (each strides over the row groups)
-static_assert(kQ6Waves <= AQ_HEAD_CANDIDATES, "one argmax key per wave");
+static_assert(kQ6Waves / 4 + AQ_HEAD_ARRIVAL_SLOTS <= AQ_HEAD_CANDIDATES, "one argmax key per workgroup");
 
 struct Q6Raw {
   uint4 l0, l1, h0, h1;  // the unit's 32 ql bytes and 32 qh bytes
@@ -106,7 +107,7 @@ struct Q6Args {
   float eps;
   float* y;
   int rows, nb;
-  uint64_t* cand;  // one argmax key per wave (NULL: none)
+  StepEnd step;    // the greedy step's end in the same launch (step.cand NULL: none)
 };
 
 // K <= 4096: UP lanes per row (the unit count rounded up to a power of two), 64 / UP rows a step, x in registers;
@@ -185,10 +186,7 @@ __global__ __launch_bounds__(256) void k_head_q6(Q6Args a) {
     process(rg + 2 * waves, rc);
     issue(rg + 5 * waves, rc);
   }
-  if (a.cand) {
-    const uint64_t m = wave_key_max(best, best_row);
-    if (lane == 0) a.cand[wave] = m;
-  }
+  if (a.step.cand) workgroup_step_end<4>(a.step, wave_key_max(best, best_row));  // workgroup-uniform
 }
 
 // Any K (% 256): x (times the norm weights) and the per-unit offsets sx staged in LDS; one row a wave step, the
@@ -245,10 +243,7 @@ __global__ __launch_bounds__(256) void k_head_q6_lds(Q6Args a) {
       if (!__builtin_isnan(v) && (best_row < 0 || v > best)) best = v, best_row = row;
     }
   }
-  if (a.cand) {
-    const uint64_t m = wave_key_max(best, best_row);
-    if (lane == 0) a.cand[wave] = m;
-  }
+  if (a.step.cand) workgroup_step_end<4>(a.step, wave_key_max(best, best_row));  // workgroup-uniform
 }
 
 // x[t] = the dequantized row ids[t] (rows outside [0, rows) read row 0): (d * sc) * (q - 32) in fp32, a thread a
@@ -296,7 +291,7 @@ int q6_check(const void* q, const void* d, int64_t rows, int64_t cols) {
   return AQ_OK;
 }
 
-// Waves a head launch over rows x cols uses (also its argmax key count).
+// Waves a head launch over rows x cols uses (a multiple of 4: workgroups of 4 waves).
 int q6_waves(int64_t rows, int64_t cols) {
   const int64_t units = cols / 64;
   int64_t per_step = 1;
@@ -333,7 +328,7 @@ int launch_head_q6(const Q6Args& a, int64_t cols, hipStream_t s) {
 
 extern "C" int64_t aq_head_q6_candidates(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0 || cols % 256) return 0;
-  return aq::q6_waves(rows, cols);
+  return aq::q6_waves(rows, cols) / 4 + AQ_HEAD_ARRIVAL_SLOTS;  // a key per workgroup, then the counters
 }
 
 extern "C" int aq_gemv_q6(const uint8_t* q, const uint16_t* d, const float* x, float* y, int64_t rows, int64_t cols,
@@ -342,7 +337,7 @@ extern "C" int aq_gemv_q6(const uint8_t* q, const uint16_t* d, const float* x, f
   if (st) return st;
   if (!x || !y) return AQ_ERR_NULL;
   if (!aq::aligned(x, 16)) return AQ_ERR_ALIGN;
-  const aq::Q6Args a{q, d, x, nullptr, 0.f, y, (int)rows, (int)(cols / 256), nullptr};
+  const aq::Q6Args a{q, d, x, nullptr, 0.f, y, (int)rows, (int)(cols / 256), {}};
   return aq::launch_head_q6(a, cols, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -352,16 +347,12 @@ extern "C" int aq_head_argmax_q6(const uint8_t* q, const uint16_t* d, const floa
                                  int32_t advance, void* stream) {
   int st = aq::q6_check(q, d, rows, cols);
   if (st) return st;
-  if (!x || !logits || !cand || !token || !pos) return AQ_ERR_NULL;
-  if (hist_cap < 0) return AQ_ERR_SHAPE;
-  if (!aq::aligned(x, 16) || !aq::aligned(cand, 8) || (norm_w && !aq::aligned(norm_w, 2))) return AQ_ERR_ALIGN;
-  const int ncand = aq::q6_waves(rows, cols);
-  if (cand_cap < ncand) return AQ_ERR_CAPACITY;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const aq::Q6Args a{q, d, x, norm_w, eps, logits, (int)rows, (int)(cols / 256), cand};
-  st = aq::launch_head_q6(a, cols, s);
+  if (!x || !logits) return AQ_ERR_NULL;
+  if (!aq::aligned(x, 16) || (norm_w && !aq::aligned(norm_w, 2))) return AQ_ERR_ALIGN;
+  aq::Q6Args a{q, d, x, norm_w, eps, logits, (int)rows, (int)(cols / 256), {}};
+  st = aq::make_step_end(cand, cand_cap, aq::q6_waves(rows, cols) / 4, token, pos, hist, hist_cap, advance, a.step);
   if (st != AQ_OK) return st;
-  return aq::launch_argmax_step(cand, ncand, token, pos, hist, hist_cap, advance, s);
+  return aq::launch_head_q6(a, cols, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int aq_embed_q6(const uint8_t* q, const uint16_t* d, int64_t rows, int64_t cols, const int32_t* ids,

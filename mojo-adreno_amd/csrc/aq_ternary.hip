@@ -16,6 +16,7 @@
 //   1024 + 4^j leaves (c - 1) * 4^j exactly, and v_dot2_f32_f16 against the x pair pre-scaled by 4^-j accumulates
 //   (c - 1) * x in fp32. Positions 5..7 are the same after one shift by 10. No bias to cancel.
 #include "aq_common.h"
+#include "aq_step_end.h"
 
 namespace aq {
 
@@ -210,10 +211,11 @@ __global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict_
 // are summed in phase order through LDS (deterministic). x pairs and the per-group biases of t2_word_dot_b are
 // staged in LDS once.
 template <int CB>
-// cand != NULL: the workgroup also leaves the argmax key of its CB outputs (first maximum) in cand[blockIdx.x].
+// step.cand != NULL: the launch also ends the greedy step (step_end), each workgroup's key the first maximum of its
+// CB outputs (kNonFiniteKey if any of them is NaN or infinite).
 __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
-                                                      int K, uint64_t* __restrict__ cand) {
+                                                      int K, StepEnd step) {
   constexpr int PH = 8 * 64 / CB;  // phases per workgroup
   extern __shared__ uint32_t xs[];   // [K/16][8] x pairs (x[16 r + p], x[16 r + p + 8]), then [K/128] group biases
   __shared__ float red[PH][CB];
@@ -263,35 +265,39 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
 #pragma unroll
     for (int p = 0; p < PH; ++p) v += red[p][threadIdx.x];
     y[blockIdx.x * CB + threadIdx.x] = v;
-    if (cand) red[0][threadIdx.x] = v;  // each thread rereads only its own column: no barrier needed before this
+    if (step.cand) red[0][threadIdx.x] = v;  // each thread rereads only its own column: no barrier needed before this
   }
-  if (cand) {  // workgroup-uniform
+  if (step.cand) {  // workgroup-uniform
     __syncthreads();
-    if (threadIdx.x == 0) {
-      const int c0 = blockIdx.x * CB, cols = min(CB, N - c0);
-      float best = red[0][0];
-      int bi = 0;
-      bool bad = !__builtin_isfinite(best);
-      for (int j = 1; j < cols; ++j) {
-        if (red[0][j] > best) best = red[0][j], bi = j;
-        bad |= !__builtin_isfinite(red[0][j]);
+    if (threadIdx.x < 64) {
+      uint64_t key = 0;
+      if (threadIdx.x == 0) {
+        const int c0 = blockIdx.x * CB, cols = min(CB, N - c0);
+        float best = red[0][0];
+        int bi = 0;
+        bool bad = !__builtin_isfinite(best);
+        for (int j = 1; j < cols; ++j) {
+          if (red[0][j] > best) best = red[0][j], bi = j;
+          bad |= !__builtin_isfinite(red[0][j]);
+        }
+        key = bad ? kNonFiniteKey : argmax_key(best, c0 + bi);
       }
-      cand[blockIdx.x] = bad ? kNonFiniteKey : argmax_key(best, c0 + bi);
+      step_end(step, key);
     }
   }
 }
 
 // Wide matrices (a vocabulary head: many columns, K <= 16384): a 256-thread workgroup owns 256 consecutive columns
 // over all of K (lane l: columns 4 l .. 4 l + 3, one 16-byte load per k-row); wave w takes the 128-groups w, w + 4,
-// ... Wave partials are summed in wave order through LDS. cand != NULL: the workgroup's argmax key (first maximum of
-// its columns; kNonFiniteKey if any of them is NaN or infinite) goes to cand[blockIdx.x]. N % 4 == 0.
+// ... Wave partials are summed in wave order through LDS. step.cand != NULL: the launch also ends the greedy step
+// (step_end), each workgroup's key the first maximum of its columns (kNonFiniteKey if any of them is NaN or
+// infinite). N % 4 == 0.
 __global__ __launch_bounds__(256) void k_t2_gemv_wide(const uint32_t* __restrict__ x2h, const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc, float* __restrict__ y, int N,
-                                                      int K, uint64_t* __restrict__ cand) {
+                                                      int K, StepEnd step) {
   constexpr int CPL = 4, COLS = 256;
   extern __shared__ uint32_t xs[];  // [K/16][8] x pairs (x[16 r + p], x[16 r + p + 8]), then [K/128] group biases
   __shared__ float red[4][COLS];
-  __shared__ uint64_t kred[4];
   const int krows = K >> 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float* gbias = reinterpret_cast<float*>(xs + krows * 8);
@@ -376,16 +382,9 @@ __global__ __launch_bounds__(256) void k_t2_gemv_wide(const uint32_t* __restrict
   const int t = threadIdx.x, n = blockIdx.x * COLS + t;  // one column a thread
   const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
   if (n < N) y[n] = v;
-  if (cand) {  // workgroup-uniform
+  if (step.cand) {  // workgroup-uniform
     const uint64_t key = n >= N ? 0ull : __builtin_isfinite(v) ? argmax_key(v, n) : kNonFiniteKey;
-    const uint64_t m = wave_max_u64(key);
-    if (lane == 0) kred[wave] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint64_t b = kred[0];
-      for (int i = 1; i < 4; ++i) b = kred[i] > b ? kred[i] : b;
-      cand[blockIdx.x] = b;
-    }
+    workgroup_step_end<4>(step, wave_max_u64(key));
   }
 }
 
@@ -491,21 +490,27 @@ inline int t2_cols_per_block(int64_t n, int64_t k) {
   return (n + 31) / 32 >= 256 ? 32 : 16;
 }
 
+// Workgroups of the launch over N columns (also the argmax keys of a head launch).
+inline int64_t t2_blocks(int64_t n, int64_t k) {
+  const int cb = t2_cols_per_block(n, k);
+  return (n + cb - 1) / cb;
+}
+
 static int launch_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* y, int N, int K,
-                          uint64_t* cand, hipStream_t sm) {
+                          const StepEnd& step, hipStream_t sm) {
   // x staging: 8 pairs per 16-k row (2K bytes), then one bias per 128-group
   const size_t lds = (size_t)(K / 16) * 8 * 4 + (size_t)(K / 128) * 4;
   if (lds > 64 * 1024) return AQ_ERR_CAPACITY;
   const int cb = t2_cols_per_block(N, K);
   if (cb == 256)
     hipLaunchKernelGGL(k_t2_gemv_wide, dim3((unsigned)((N + 255) / 256)), dim3(256), lds, sm, x2h, w, s, y, N, K,
-                       cand);
+                       step);
   else if (cb == 32)
     hipLaunchKernelGGL(k_t2_gemv_cols<32>, dim3((unsigned)((N + 31) / 32)), dim3(512), lds, sm, x2h, w, s, y, N, K,
-                       cand);
+                       step);
   else
     hipLaunchKernelGGL(k_t2_gemv_cols<16>, dim3((unsigned)((N + 15) / 16)), dim3(512), lds, sm, x2h, w, s, y, N, K,
-                       cand);
+                       step);
   return launch_status();
 }
 }  // namespace aq
@@ -517,11 +522,11 @@ extern "C" int aq_t2_gemv(const uint32_t* x2h, const uint32_t* w, const uint16_t
   int st = t2_check(x2h, w, s, n, k);
   if (st) return st;
   if (!y) return AQ_ERR_NULL;
-  return launch_t2_gemv(x2h, w, s, y, (int)n, (int)k, nullptr, reinterpret_cast<hipStream_t>(stream));
+  return launch_t2_gemv(x2h, w, s, y, (int)n, (int)k, StepEnd{}, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t aq_t2_head_candidates(int64_t n, int64_t k) {
-  return n > 0 ? (n + aq::t2_cols_per_block(n, k) - 1) / aq::t2_cols_per_block(n, k) : 0;
+  return n > 0 ? aq::t2_blocks(n, k) + AQ_HEAD_ARRIVAL_SLOTS : 0;  // a key per workgroup, then the counters
 }
 
 extern "C" int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* logits, int64_t n,
@@ -529,15 +534,11 @@ extern "C" int aq_t2_head_argmax(const uint32_t* x2h, const uint32_t* w, const u
                                  int32_t* hist, int32_t hist_cap, int32_t advance, void* stream) {
   int st = t2_check(x2h, w, s, n, k);
   if (st) return st;
-  if (!logits || !cand || !token || !pos) return AQ_ERR_NULL;
-  if (hist_cap < 0) return AQ_ERR_SHAPE;
-  const int64_t ncand = aq_t2_head_candidates(n, k);
-  if (cand_cap < ncand) return AQ_ERR_CAPACITY;
-  if (!aligned(cand, 8)) return AQ_ERR_ALIGN;
-  hipStream_t sm = reinterpret_cast<hipStream_t>(stream);
-  st = launch_t2_gemv(x2h, w, s, logits, (int)n, (int)k, cand, sm);
+  if (!logits) return AQ_ERR_NULL;
+  StepEnd step{};
+  st = make_step_end(cand, cand_cap, t2_blocks(n, k), token, pos, hist, hist_cap, advance, step);
   if (st != AQ_OK) return st;
-  return launch_argmax_step(cand, (int)ncand, token, pos, hist, hist_cap, advance, sm);
+  return launch_t2_gemv(x2h, w, s, logits, (int)n, (int)k, step, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int aq_t2_packed_linear(const uint32_t* x2h, const uint32_t* w, const uint16_t* s, float* partials,

@@ -126,18 +126,18 @@ def test_t2_head_argmax_validation():
     lib = aq.lib()
     buf = ctypes.create_string_buffer(4096 + 16)
     p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
-    # one argmax key per workgroup: 256 columns each when N % 4 == 0 gives >= 512 workgroups (K <= 16384), else 32
-    # once that gives >= 256 workgroups, else 16
-    assert lib.aq_t2_head_candidates(248320, 2048) == 970
-    assert lib.aq_t2_head_candidates(248320, 32768) == 7760
-    assert lib.aq_t2_head_candidates(151669, 2048) == 4740
-    assert lib.aq_t2_head_candidates(8000, 1024) == 500
-    assert lib.aq_t2_head_candidates(8192, 512) == 256
-    assert lib.aq_t2_head_candidates(7, 128) == 1
+    # one argmax key per workgroup (256 columns each when N % 4 == 0 gives >= 512 workgroups (K <= 16384), else 32
+    # once that gives >= 256 workgroups, else 16), then 17 arrival counter slots
+    assert lib.aq_t2_head_candidates(248320, 2048) == 970 + 17
+    assert lib.aq_t2_head_candidates(248320, 32768) == 7760 + 17
+    assert lib.aq_t2_head_candidates(151669, 2048) == 4740 + 17
+    assert lib.aq_t2_head_candidates(8000, 1024) == 500 + 17
+    assert lib.aq_t2_head_candidates(8192, 512) == 256 + 17
+    assert lib.aq_t2_head_candidates(7, 128) == 1 + 17
     assert lib.aq_t2_head_candidates(0, 128) == 0
-    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 499, p, p, None, 0, 1, None) == 6   # too few keys
-    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 500, p, None, None, 0, 1, None) == 5  # no pos
-    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p + 4, 500, p, p, None, 0, 1, None) == 3  # misaligned keys
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 516, p, p, None, 0, 1, None) == 6   # too few slots
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p, 517, p, None, None, 0, 1, None) == 5  # no pos
+    assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1024, p + 4, 517, p, p, None, 0, 1, None) == 3  # misaligned keys
     assert lib.aq_t2_head_argmax(p, p, p, p, 8000, 1000, p, 500, p, p, None, 0, 1, None) == 1     # K % 128
     assert lib.aq_t2_head_argmax(p, p, p, None, 8000, 1024, p, 500, p, p, None, 0, 1, None) == 5  # no logits
 
@@ -148,17 +148,17 @@ def test_q6_validation():
     buf = ctypes.create_string_buffer(4096 + 16)
     p = (ctypes.addressof(buf) + 15) & ~15  # host memory: never dereferenced, every call must fail first
     f = ctypes.c_float(1e-5)
-    # one argmax key per wave, at most 3072 waves: 65536 rows x 2048 (2 rows a wave step) -> 3072; 7 rows x 256
-    # (16 a step) -> 4
-    assert lib.aq_head_q6_candidates(65536, 2048) == 3072
-    assert lib.aq_head_q6_candidates(7, 256) == 4
-    assert lib.aq_head_q6_candidates(1000, 5120) == 1000
+    # one argmax key per workgroup of 4 waves, at most 3072 waves: 65536 rows x 2048 (2 rows a wave step) -> 768
+    # workgroups; 7 rows x 256 (16 a step) -> 1; then 17 arrival counter slots
+    assert lib.aq_head_q6_candidates(65536, 2048) == 3072 // 4 + 17
+    assert lib.aq_head_q6_candidates(7, 256) == 1 + 17
+    assert lib.aq_head_q6_candidates(1000, 5120) == 1000 // 4 + 17
     assert lib.aq_head_q6_candidates(10, 100) == 0
     assert lib.aq_gemv_q6(p, p, p, p, 100, 1000, None) == 1              # cols % 256
     assert lib.aq_gemv_q6(p + 8, p, p, p, 100, 2048, None) == 3          # q not 16-byte aligned
     assert lib.aq_gemv_q6(p, p, None, p, 100, 2048, None) == 5
     assert lib.aq_gemv_q6(p, p, p, p, 1 << 24, 2048, None) == 6          # q beyond 2 GiB
-    assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 3071, p, p, None, 0, 1, None) == 6
+    assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 768 + 16, p, p, None, 0, 1, None) == 6
     assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p + 4, 4096, p, p, None, 0, 1, None) == 3
     assert lib.aq_head_argmax_q6(p, p, p, None, f, p, 65536, 2048, p, 4096, p, None, None, 0, 1, None) == 5
     assert lib.aq_embed_q6(p, p, 100, 2048, p, 0, p, None) == 1            # no tokens

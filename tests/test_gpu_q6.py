@@ -81,6 +81,44 @@ def test_head_argmax_q6_kat(dev, rows, cols):
     assert hist[3] == tok and (np.delete(hist, 3) == -9).all()
 
 
+@pytest.mark.parametrize("rows,cols", [(65536, 2048), (3000, 5120)])
+def test_head_argmax_q6_one_launch_repeats(dev, rows, cols):
+    """The head ends the greedy step in its own launch (the last workgroup to arrive picks the token): the arrival
+    counters in cand's last HEAD_ARRIVAL_SLOTS slots are back at zero after every call, so calls in a row, eager and
+    replayed from one graph, each give the exact first maximum and advance the position (768 and 750 workgroups)."""
+    import torch
+    from aq import ops
+    rng = np.random.default_rng(rows + 1)
+    q, d, x0 = _kat(rng, rows, cols)
+    xs = [x0] + [rng.integers(-3, 4, size=cols).astype(np.float32) for _ in range(2)]
+    want = [orc.argmax_first(_exact(q, d, xv).astype(np.float32)) for xv in xs]
+    Q, D = to_dev(q, dev), to_dev(d, dev)
+    x = torch.empty(cols, dtype=torch.float32, device=dev)
+    logits = torch.empty(rows, dtype=torch.float32, device=dev)
+    cand = torch.zeros(ops.head_q6_candidates(rows, cols), dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.full((8,), -1, dtype=torch.int32, device=dev)
+    nonorm = torch.empty(0, dtype=torch.float16, device=dev)
+    run = lambda: torch.ops.aq.head_argmax_q6(Q, D, x, nonorm, 1e-5, logits, cand, tok, pos, hist, 1)  # noqa
+    for i, xv in enumerate(xs):  # eager
+        x.copy_(to_dev(xv, dev))
+        run()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    pos.zero_()
+    for i, xv in enumerate(xs):  # replays
+        x.copy_(to_dev(xv, dev))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
+    np.testing.assert_array_equal(to_np(hist)[:3], np.array(want, np.int32))
+
+
 def test_head_argmax_q6_ties_pick_the_first(dev):
     """Rows 5, 2000 and 40000 are copies of the largest row: the token is 5 (the rows sit in different waves)."""
     rng = np.random.default_rng(8)

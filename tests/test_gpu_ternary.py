@@ -192,6 +192,45 @@ def test_t2_head_argmax_kat(dev, n, k):
     assert hist[5] == tok and (np.delete(hist, 5) == -9).all()
 
 
+@pytest.mark.parametrize("n", [248320, 151669])
+def test_t2_head_argmax_one_launch_repeats(dev, n):
+    """The head ends the greedy step in its own launch (the last workgroup to arrive picks the token): the arrival
+    counters are back at zero after every call, so calls in a row, eager and replayed from one graph, each give the
+    exact first maximum and advance the position. 248320 columns take 970 workgroups of 256 columns; 151669 take
+    4740 of 32 (the last workgroup reads the keys in five passes)."""
+    import torch
+    ops = _ops()
+    rng = np.random.default_rng(n + 2)
+    k = 256
+    codes, s, x0 = _kat(rng, n, k)
+    xs = [x0] + [rng.integers(-3, 4, size=k).astype(np.float32) for _ in range(2)]
+    want = [orc.argmax_first(_exact(codes, s, xv).astype(np.float32)) for xv in xs]
+    W, S = to_dev(orc.t2w_pack(codes), dev), to_dev(s, dev)
+    xh = torch.empty(k // 2, dtype=torch.int32, device=dev)
+    logits = torch.empty(n, dtype=torch.float32, device=dev)
+    cand = torch.zeros(ops.t2_head_candidates(n, k), dtype=torch.int64, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    hist = torch.full((8,), -9, dtype=torch.int32, device=dev)
+    run = lambda: torch.ops.aq.t2_head_argmax(xh, W, S, logits, cand, tok, pos, hist, 1)  # noqa
+    for i, xv in enumerate(xs):  # eager
+        xh.copy_(to_dev(orc.x2h_pack(xv), dev).view(torch.int32))
+        run()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    pos.zero_()
+    for i, xv in enumerate(xs):  # replays
+        xh.copy_(to_dev(orc.x2h_pack(xv), dev).view(torch.int32))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want[i] and int(pos.item()) == i + 1
+        assert not to_np(cand)[-ops.HEAD_ARRIVAL_SLOTS:].any()
+    np.testing.assert_array_equal(to_np(hist)[:3], np.array(want, np.int32))
+
+
 @pytest.mark.parametrize("n", [8000, 248320])
 def test_t2_head_argmax_ties_pick_the_first(dev, n):
     """Columns 3, 40, 900 and 7000 (and 140000) are all +1 codes, the largest product: the token is 3, across
