@@ -313,22 +313,29 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   }
 #undef AQ_WAIT_X_SYNC
   if constexpr (W8) {
-    // the last step's barrier follows its wait for the X loads: LDS is quiescent and no wave reads it any more
-    float4v* red = reinterpret_cast<float4v*>(xbuf);  // 4 * FR slots = 4 waves x MB x NB x 64 lanes
-    if (grp == 1) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) red[((wave * MB + mb) * NB + nb) * 64 + lane] = acc[mb][nb];
-    }
-    __syncthreads();
-    if (grp == 1) return;
+    // The two groups' sums meet in LDS, each group finishing half of the columns: group 0 column blocks 0 .. NB/2 - 1,
+    // group 1 the rest; each first leaves the other's half in LDS. (One group finishing all of them left the other
+    // idle through the final stores.) The last step's barrier follows its wait for the X loads: LDS is quiescent and
+    // no wave reads it any more. Register arrays are indexed by constants only, so the group picks by selects.
+    constexpr int H = NB / 2;
+    float4v* red = reinterpret_cast<float4v*>(xbuf);  // [group][wave][MB][H][64]: 4 * FR slots
+    const bool g1 = grp != 0;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] += red[((wave * MB + mb) * NB + nb) * 64 + lane];
+      for (int h = 0; h < H; ++h)
+        red[(((grp * 4 + wave) * MB + mb) * H + h) * 64 + lane] = g1 ? acc[mb][h] : acc[mb][H + h];
+    __syncthreads();
+    float4v out[MB][H];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+        out[mb][h] = (g1 ? acc[mb][H + h] : acc[mb][h]) + red[((((1 - grp) * 4 + wave) * MB + mb) * H + h) * 64 + lane];
+    gemm_store<MB, H, ADD, SPLIT, MODE>(ga, out, m0, nw0 + grp * 16 * H, sp, lane);
+  } else {
+    gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
   }
-  gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
 }
 
 template <int FMT, int MB, int NB, int MODE, bool W8>
