@@ -113,3 +113,29 @@ def test_no_workspace_single_pass(dev):
     torch.ops.aq.gemm_q4(to_dev(x, dev), to_dev(orc.q4w_pack(vals), dev), to_dev(ws, dev), y, 32, False, tiny)
     np.testing.assert_array_equal(to_np(y), exact_int4_product(vals, ws, x.astype(np.float32), 32)
                                   .astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k,group,xf32", [
+    (431, 512, 2048, 32, False),   # fp16 X, the direct-to-LDS kernel in its eight-wave form
+    (431, 2048, 8192, 32, False),  # K split: fp32 partials summed in split order
+    (200, 384, 1024, 64, True),    # fp32 X (the reference's p_gemm_q4 interface), rounded to fp16 when staged
+    (128, 256, 2048, 128, False),
+    (90, 128, 2112, 64, False),    # K % 128 != 0: the general kernel
+])
+def test_elementwise_error_bound(dev, m, n, k, group, xf32):
+    """Every output, not only the largest, within 1e-3 of its own scale: |y - ref| <= 1e-3 * (|X| . |W|^T)
+    elementwise, against float64 over the exact dequantised weights. The error sources bound it: each dequantised
+    weight rounded to fp16 (2^-11 relative), fp32 X rounded to fp16 (2^-11), fp32 accumulation. X spans four decades,
+    and the bound is relative to |X| . |W|^T rather than |y|, so it also holds the outputs whose sums nearly cancel."""
+    from aq import synth
+    rng = np.random.default_rng(m + n + k + group + (7 if xf32 else 0))
+    wq, ws = synth.int4_matrix(rng, n, k, group)
+    x = (rng.standard_normal((m, k)) * 10.0 ** rng.uniform(-2, 2, size=(m, k))).astype(
+        np.float32 if xf32 else np.float16)
+    got = _gemm(x, wq, ws, group, dev).astype(np.float64)
+    w = orc.q4w_dequant(wq, ws, group).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd @ w.T
+    scale = np.abs(xd) @ np.abs(w).T
+    worst = float(np.max(np.abs(got - ref) / scale))
+    assert worst <= 1e-3, worst

@@ -280,3 +280,22 @@ def test_t2_head_argmax_float_logits(dev, wide):
     lg = to_np(logits)
     assert rel_inf(lg, orc.ternary_gemv(w, s, xh, n, k)) < TOL
     assert int(tok.item()) == orc.argmax_first(lg) and int(pos.item()) == 0
+
+
+@pytest.mark.parametrize("m,n,k,xf32", [(412, 1024, 4096, False), (412, 256, 12288, False), (100, 300, 1024, True)])
+def test_gemm_t2_elementwise_error_bound(dev, m, n, k, xf32):
+    """Every output within 1e-3 of its own scale, |y - ref| <= 1e-3 * (|X| . |W|^T) elementwise, against float64: the
+    ternary weights times their fp16 scales are exact in fp16, so only fp32 accumulation (and, for fp32 X, its rounding
+    to fp16) contribute. X spans four decades."""
+    from aq import synth
+    rng = np.random.default_rng(m + n + k + (3 if xf32 else 0))
+    w, s = synth.ternary_matrix(rng, n, k)
+    x = (rng.standard_normal((m, k)) * 10.0 ** rng.uniform(-2, 2, size=(m, k))).astype(
+        np.float32 if xf32 else np.float16)
+    got = _gemm_t2(x, w, s, dev).astype(np.float64)
+    wd = orc.t2w_dequant(w, s).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd @ wd.T
+    scale = np.abs(xd) @ np.abs(wd).T
+    worst = float(np.max(np.abs(got - ref) / scale))
+    assert worst <= 1e-3, worst
