@@ -70,6 +70,14 @@ __device__ __forceinline__ half8 dequant_t2_natural(uint32_t w, int h, uint32_t 
 // leaves most of the VALU work outside the MFMA shadow. The caller gives W8 an even number of super-steps.
 // NB = 2 (narrow tiles, four waves, dense only): each wave takes 32 columns, a workgroup 128, so shapes with few
 // 256-column tiles need fewer K splits (and fp32 partials) to fill the chip.
+// The lane index computed where it is used (not merged with an earlier computation), so that nothing derived from
+// the thread index has to stay in a register across the main loop.
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 template <int FMT, int MB, int NB, bool ADD, bool SPLIT, int MODE, bool W8>
 __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   const uint32_t* __restrict__ wq = ga.w;
@@ -87,8 +95,10 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
   int ks0 = sp * ga.sup_per_split;
   int ks1 = min(nsup, ks0 + ga.sup_per_split);
   const int lane = threadIdx.x & 63;
-  const int grp = W8 ? (int)(threadIdx.x >> 8) : 0;  // the half of the super-steps this wave's group takes
-  const int wave = (threadIdx.x >> 6) & 3;             // the wave within its group of four
+  // wave-uniform, in scalar registers: the epilogue needs them after the loop, and no vector register has to hold
+  // them (or the thread index) through it
+  const int grp = W8 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) : 0;  // this group's half of the K range
+  const int wave = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));     // the wave within its group
   if constexpr (W8) {
     const int half = (ks1 - ks0) >> 1;
     ks0 += grp * half;
@@ -122,7 +132,7 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
     if constexpr (MODE != kDense) m = g < ga.rows_total ? (ga.src ? ga.src[g] : g) : -1;
     xoff[mb] = ((m >= 0 && m < M) ? (uint32_t)m * (uint32_t)K * 2u : kOOB) + (uint32_t)spiece * 16u;
   }
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wave_u = wave;
   auto stage = [&](int ks, uint4* dst, int mb) {
     const int k = ks * kSuper + 32 * wave_u;  // K % 128 == 0: always inside the row
     lds_load16(x_rsrc, dst + (mb * 4 + wave_u) * 64, xoff[mb] + (uint32_t)k * 2u);
@@ -320,29 +330,30 @@ __global__ __launch_bounds__(W8 ? 512 : 256) void k_gemm_x16(GemmArgs ga) {
     constexpr int H = NB / 2;
     float4v* red = reinterpret_cast<float4v*>(xbuf);  // [group][wave][MB][H][64]: 4 * FR slots
     const bool g1 = grp != 0;
+    const int el = fresh_lane_id();
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int h = 0; h < H; ++h)
-        red[(((grp * 4 + wave) * MB + mb) * H + h) * 64 + lane] = g1 ? acc[mb][h] : acc[mb][H + h];
+        red[(((grp * 4 + wave) * MB + mb) * H + h) * 64 + el] = g1 ? acc[mb][h] : acc[mb][H + h];
     __syncthreads();
     float4v out[MB][H];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int h = 0; h < H; ++h)
-        out[mb][h] = (g1 ? acc[mb][H + h] : acc[mb][h]) + red[((((1 - grp) * 4 + wave) * MB + mb) * H + h) * 64 + lane];
-    gemm_store<MB, H, ADD, SPLIT, MODE>(ga, out, m0, nw0 + grp * 16 * H, sp, lane);
+        out[mb][h] = (g1 ? acc[mb][H + h] : acc[mb][h]) + red[((((1 - grp) * 4 + wave) * MB + mb) * H + h) * 64 + el];
+    gemm_store<MB, H, ADD, SPLIT, MODE>(ga, out, m0, nw0 + grp * 16 * H, sp, el);
   } else {
-    gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, lane);
+    gemm_store<MB, NB, ADD, SPLIT, MODE>(ga, acc, m0, nw0, sp, fresh_lane_id());
   }
 }
 
 template <int FMT, int MB, int NB, int MODE, bool W8>
 static void launch_mb(const GemmArgs& ga, bool add, bool split, int blocks, hipStream_t s) {
   const dim3 block(W8 ? 512 : 256);
-  if constexpr (NB == 2 && MODE != kDense && W8) {
-    return;  // not built: grouped launches keep four waves
+  if constexpr (MODE != kDense && W8) {
+    return;  // not built: grouped launches keep four waves (launch_gemm_x16 takes eight only for dense tiles)
   } else if constexpr (MODE == kDense) {
     if (split) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, false, true, MODE, W8>), dim3(blocks), block, 0, s, ga);
     else if (add) hipLaunchKernelGGL((k_gemm_x16<FMT, MB, NB, true, false, MODE, W8>), dim3(blocks), block, 0, s, ga);
