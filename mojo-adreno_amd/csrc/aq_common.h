@@ -10,6 +10,10 @@ namespace aq {
 
 constexpr int kWave = 64;
 
+// This wave's index within its workgroup as a scalar (wave-uniform) value. The compiler does not infer that
+// threadIdx.x / 64 is the same across a wave: loops and branches on the vector value run under exec masks.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
   const int ks0 = sp * sup_per_split;
   const int ks1 = min(nsup, ks0 + sup_per_split);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   // this wave's first column; SwiGLU: gate columns j0 .. j0 + NW/2 - 1 and up columns F + j0 ..
   const int nw0 = MODE == kGroupedSwiglu ? nt * (2 * NW) + wave * (NW / 2) : nt * (4 * NW) + wave * NW;
   const int kw = K >> 3;                       // Q4W words per row

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
   // digit products (v_dot8_i32_i4) for the G32 modes but kMoeDown
   constexpr bool kDigits = G32 && MODE != kMoeDown;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int gpr = k / group;
   constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
   constexpr int SL = MODE == kMoeDown ? T : 1;  // weight rows per output (kMoeDown: one per expert slot)
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
   const int kw = k >> 3, nch = k >> 5, gpr = k >> gsh;
   uint4* xd = reinterpret_cast<uint4*>(lds4);
   float* xf = reinterpret_cast<float*>(xd + 6 * nch);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rp = wave % RP, ks = wave / RP;  // row pair, K slice
   const int c0 = (int)(((int64_t)nch * ks) / KS), c1 = (int)(((int64_t)nch * (ks + 1)) / KS);
 

@@ -21,7 +21,7 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
                                                float* __restrict__ weights, int tokens, int E, int topk,
                                                const float* __restrict__ x, uint32_t* __restrict__ xq, int d) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = blockIdx.x * 4 + wave_id();
   if (t >= tokens) return;  // wave-uniform; the kernel has no barrier
   if (xq) {
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * d);
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t* __restrict__ 
   __shared__ int32_t wtot[16][3];
   __shared__ int repeated;       // some token chose one expert twice: ordered scan
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   if (threadIdx.x == 0) repeated = 0;
   for (int i = threadIdx.x; i < E * W; i += 1024) bits[i] = 0ull;
   for (int r = threadIdx.x; r < o.max_rows; r += 1024) o.src[r] = -1;  // padding rows; real rows are set below
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
 __global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ w, const float* __restrict__ x,
                                                   float* __restrict__ y, int n, int k, int tokens) {
   const int lane = threadIdx.x & 63;
-  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int o = blockIdx.x * 4 + wave_id();
   if (o >= n * tokens) return;
   const int t = o / n, r = o - t * n;
   const float* wr = w + (size_t)r * k;

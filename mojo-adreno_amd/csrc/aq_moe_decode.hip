@@ -30,7 +30,7 @@ __global__ __launch_bounds__(512) void k_moe_down_dec(const uint32_t* __restrict
   extern __shared__ uint4 xd[];  // stage_digits planes of the 8 slots ([slot][6][f / 32]), then their factors
   __shared__ float red[kDownSlots][kDownRows];
   const int lane = threadIdx.x & 63;
-  const int s = threadIdx.x >> 6;  // expert slot of this wave
+  const int s = wave_id();  // expert slot of this wave
   const int r0 = blockIdx.x * kDownRows;
   const int row = lane >> 3, sub = lane & 7;
   const int kw = f >> 3, nch = f >> 5, gpr = f >> gsh;

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void k_head_q6(Q6Args a) {
   const auto qr = make_rsrc(a.q, (uint32_t)((int64_t)a.rows * a.nb * kQ6Bytes));
   const auto dr = make_rsrc(a.d, (uint32_t)((int64_t)a.rows * a.nb * 2));
   const int groups = (a.rows + RPW - 1) / RPW;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), waves = gridDim.x * 4;
+  const int wave = blockIdx.x * 4 + wave_id(), waves = gridDim.x * 4;
   auto issue = [&](int rg, Q6Raw& r) {
     const int row = rg * RPW + sub;
     const bool ok = live && rg < groups && row < a.rows;
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void k_head_q6(Q6Args a) {
 __global__ __launch_bounds__(256) void k_head_q6_lds(Q6Args a) {
   extern __shared__ float xs[];  // K floats, then 4 * (K / 64) floats of sx
   __shared__ float red[4];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = wave_id();
   const int U = 4 * a.nb, K = 256 * a.nb;
   float4* sxs = reinterpret_cast<float4*>(xs + K);
   float ss = 0.f;

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void k_t2_partials(const uint32_t* __restrict_
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int n0 = ct * 256 + lane * 4;
   const int groups = (nrows + 7) >> 3;              // 128-groups in this workgroup
   const int gpw = (groups + 3) >> 2;                // groups per wave
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(512) void k_t2_gemv_cols(const uint32_t* __restrict
   t2_stage_x(x2h, xs, gbias, krows, threadIdx.x, 512);
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int c = lane % CB;
   const int ph = wave * (64 / CB) + lane / CB;
   const int n = blockIdx.x * CB + c;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void k_t2_gemv_wide(const uint32_t* __restrict
   extern __shared__ uint32_t xs[];  // [K/16][8] x pairs (x[16 r + p], x[16 r + p + 8]), then [K/128] group biases
   __shared__ float red[4][COLS];
   const int krows = K >> 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   float* gbias = reinterpret_cast<float*>(xs + krows * 8);
   const int n0 = blockIdx.x * COLS + lane * CPL;
   const bool ok = n0 < N;
