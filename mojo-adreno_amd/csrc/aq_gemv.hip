@@ -727,7 +727,9 @@ static int launch_t(const uint32_t* wq, const uint16_t* ws, const float* x, floa
     constexpr int RO = (MODE == kGateUp || MODE == kMoeGateUp) ? R / 2 : R;
     const int64_t waves = 4 * (int64_t)gemv_blocks(n_out, RO);
     const int64_t items = ((k / 32 + 63) / 64) * ((n_out + waves * RO - 1) / (waves * RO));
-    if (items >= 4 && R <= 2) return launch_x<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    if constexpr (R <= 2) {  // four register sets only for one or two rows a wave (not built otherwise)
+      if (items >= 4) return launch_x<G32, R, T, MODE, 4>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
+    }
     if (items >= 2) return launch_x<G32, R, T, MODE, 2>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
   }
   return launch_x<G32, R, T, MODE, 1>(wq, ws, x, y, n_out, k, group, f, tokens, moe, fz, s);
