@@ -101,6 +101,41 @@ def test_split_k_kat(dev, m, n, k):
                                   .astype(np.float32))
 
 
+def test_split_k_leftover_workspace_and_graph(dev):
+    """Split-K over a workspace the caller never clears: a workspace full of leftover bytes, calls in a row over it
+    (the second adding onto Y), and replays of one captured call with new X each give the exact product."""
+    import torch
+    from aq import _lib
+    m, n, k = 431, 512, 8192
+    need = _lib.lib().aq_gemm_q4_workspace_bytes(m, n, k)
+    assert need > 0
+    rng = np.random.default_rng(77)
+    vals, ws, x = kat_int4(rng, n, k, 32, tokens=m)
+    x = x.astype(np.float16)
+    want = exact_int4_product(vals, ws, x.astype(np.float32), 32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    wsp = torch.randint(0, 256, (need,), dtype=torch.uint8, device=dev, generator=gen)
+    X, W, S = to_dev(x, dev), to_dev(orc.q4w_pack(vals), dev), to_dev(ws, dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    torch.ops.aq.gemm_q4(X, W, S, y, 32, False, wsp)
+    np.testing.assert_array_equal(to_np(y), want.astype(np.float32))
+    y0 = rng.integers(-4, 4, size=(m, n)).astype(np.float32)
+    y.copy_(to_dev(y0, dev))
+    torch.ops.aq.gemm_q4(X, W, S, y, 32, True, wsp)
+    np.testing.assert_array_equal(to_np(y), (want + y0).astype(np.float32))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        torch.ops.aq.gemm_q4(X, W, S, y, 32, False, wsp)
+    for i in range(3):
+        xi = rng.integers(-3, 4, size=(m, k)).astype(np.float16)
+        X.copy_(to_dev(xi, dev))
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_np(y), exact_int4_product(vals, ws, xi.astype(np.float32), 32)
+                                      .astype(np.float32), err_msg=f"replay {i}")
+
+
 def test_no_workspace_single_pass(dev):
     """A workspace smaller than asked for falls back to one pass over K, with the same result."""
     import torch
