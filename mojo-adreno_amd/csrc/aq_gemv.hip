@@ -341,10 +341,15 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
       for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
     int cb = base0, cc = 0;  // the chunk to use next
     bool more = cb < n_out;
+    // Every pass of the loop requests all D register sets, also past the wave's last chunk (out-of-range offsets: no
+    // traffic), so that each way round the loop leaves the same loads in flight in the same order. Requests inside
+    // `more` let the loop come back to its top with only some sets requested; the compiler's wait counts, which
+    // merge all ways round, then waited for every load before the use of set 0.
     while (more) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {  // register set d by name: set d always holds the chunk d steps ahead
-        if (more) {
+        const bool act = more;       // wave-uniform
+        if (act) {
           const int c = lane + cc * kWave;
           if (c < nch) {
             uint16_t s16[R];
@@ -352,17 +357,17 @@ __global__ __launch_bounds__(256) void k_gemv_q4(const uint32_t* __restrict__ wq
             for (int r = 0; r < R; ++r) s16[r] = (uint16_t)(sd[d][r] >> sh[d][r]);
             use_chunk(c, wd[d], s16, acc);
           }
-          if (D > 1 || cb + (cc + 1 == cpl ? stride : 0) < n_out) issue_next(wd[d], sd[d], sh[d]);
-          if (++cc == cpl) {
-            finish(cb, acc);
+        }
+        if (D > 1 || (act && cb + (cc + 1 == cpl ? stride : 0) < n_out)) issue_next(wd[d], sd[d], sh[d]);
+        if (act && ++cc == cpl) {
+          finish(cb, acc);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+          for (int r = 0; r < R; ++r)
 #pragma unroll
-              for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
-            cc = 0;
-            cb += stride;
-            more = cb < n_out;
-          }
+            for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
+          cc = 0;
+          cb += stride;
+          more = cb < n_out;
         }
       }
     }
