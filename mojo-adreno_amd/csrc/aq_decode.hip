@@ -418,9 +418,11 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ qk
 #pragma unroll
     for (int h = 0; h < HPG; ++h) {
       const float mn = fmaxf(m[h], wave_max(fmaxf(sc[0][h], sc[1][h])));
-      if (mn == -INFINITY) continue;  // wave-uniform: no position of this wave so far
-      const float r = expf(m[h] - mn);  // 0 while m was -inf
-      const float p0 = expf(sc[0][h] - mn), p1 = expf(sc[1][h] - mn);  // 0 for masked positions
+      // mn = -inf (wave-uniform): no position of this wave so far, and l, acc are still 0. Measuring from 0 then gives
+      // r = p0 = p1 = 0 and leaves them so; without a branch the heads' maximum and exponent chains interleave.
+      const float mr = mn == -INFINITY ? 0.f : mn;
+      const float r = expf(m[h] - mr);  // 0 while m was -inf
+      const float p0 = expf(sc[0][h] - mr), p1 = expf(sc[1][h] - mr);  // 0 for masked positions
       l[h] = l[h] * r + (c == 0 ? p0 + p1 : 0.f);
       m[h] = mn;
       float v0[8], v1[8];
