@@ -281,6 +281,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs ga) {
 }
 
 // y[i] = (add ? y[i] : 0) + sum_{s < splits} part[s][i], summed in split order (deterministic).
+// S > 0: the split count at compile time, so every partial of a thread's four outputs is requested before the first
+// add (a loop over a run-time count waited for each load before requesting the next). S = 0: any count. The sums
+// run in split order either way.
+template <int S>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, float* __restrict__ y,
                                                        int64_t count, int splits, int add) {
   const int64_t n4 = count >> 2;
@@ -288,9 +292,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
   float4* y4 = reinterpret_cast<float4*>(y);
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
     float4 acc = add ? y4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < splits; ++s) {
-      const float4 v = p4[(int64_t)s * n4 + i];
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    if constexpr (S > 0) {
+      float4 v[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) v[s] = p4[(int64_t)s * n4 + i];
+#pragma unroll
+      for (int s = 0; s < S; ++s) acc.x += v[s].x, acc.y += v[s].y, acc.z += v[s].z, acc.w += v[s].w;
+    } else {
+      for (int s = 0; s < splits; ++s) {
+        const float4 v = p4[(int64_t)s * n4 + i];
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
     }
     y4[i] = acc;
   }
@@ -407,7 +419,17 @@ static int gemm_dispatch(const void* x, const uint32_t* wq, const uint16_t* ws, 
     int64_t blocks = (count / 4 + 255) / 256;
     if (blocks > 2048) blocks = 2048;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, s, part, y, count, p.splits, add);
+    const dim3 grid((unsigned)blocks), block(256);
+    switch (p.splits) {
+      case 2: hipLaunchKernelGGL(k_splitk_reduce<2>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 3: hipLaunchKernelGGL(k_splitk_reduce<3>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 4: hipLaunchKernelGGL(k_splitk_reduce<4>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 5: hipLaunchKernelGGL(k_splitk_reduce<5>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 6: hipLaunchKernelGGL(k_splitk_reduce<6>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 7: hipLaunchKernelGGL(k_splitk_reduce<7>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      case 8: hipLaunchKernelGGL(k_splitk_reduce<8>, grid, block, 0, s, part, y, count, p.splits, add); break;
+      default: hipLaunchKernelGGL(k_splitk_reduce<0>, grid, block, 0, s, part, y, count, p.splits, add);
+    }
     return launch_status();
   }
   return add ? gemm_mb<FMT, G32, XF32, true, false>(x, wq, ws, y, part, M, N, K, group, p, s)
