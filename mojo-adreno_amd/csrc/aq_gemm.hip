@@ -299,6 +299,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 #pragma unroll
       for (int s = 0; s < S; ++s) acc.x += v[s].x, acc.y += v[s].y, acc.z += v[s].z, acc.w += v[s].w;
     } else {
+#pragma unroll 8
       for (int s = 0; s < splits; ++s) {
         const float4 v = p4[(int64_t)s * n4 + i];
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;

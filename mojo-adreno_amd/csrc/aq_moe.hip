@@ -297,6 +297,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ w, c
   const float* xr = x + (size_t)t * k;
   float acc = 0.f;
   if ((k & 3) == 0) {
+#pragma unroll 8  // eight rows' words requested together (the multiply-add order is unchanged)
     for (int c = lane; c < (k >> 2); c += 64) {
       const float4 a = reinterpret_cast<const float4*>(wr)[c];
       const float4 b = reinterpret_cast<const float4*>(xr)[c];

@@ -394,7 +394,8 @@ __global__ __launch_bounds__(256) void k_t2_reduce(const float* __restrict__ par
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
   float acc = 0.f;
-  for (int g = 0; g < groups; ++g) acc += part[(size_t)g * N + n];
+#pragma unroll 8
+  for (int g = 0; g < groups; ++g) acc += part[(size_t)g * N + n];  // unrolled: eight partials requested together
   y[n] = acc;
 }
 
