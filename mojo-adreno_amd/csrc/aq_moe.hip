@@ -26,6 +26,7 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
   if (xq) {
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * d);
     uint4* qr = reinterpret_cast<uint4*>(xq + (size_t)t * (d / 2));
+#pragma unroll 4  // several words' loads in flight together
     for (int i = lane; i < d / 8; i += 64) {
       const float4 a = xr[2 * i], b = xr[2 * i + 1];
       qr[i] = make_uint4((uint32_t)float_to_half_bits(a.x) | ((uint32_t)float_to_half_bits(a.y) << 16),

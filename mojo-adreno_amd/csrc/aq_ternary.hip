@@ -427,11 +427,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_pack(const float* __restrict__ 
   const float* xr = x + (size_t)blockIdx.x * n;
   uint32_t* qr = q + (size_t)blockIdx.x * (n / 2);
   float ss = 0.f;
+#pragma unroll 8  // loads in flight together; the multiply-add order is unchanged
   for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float r = rsqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)n + eps);
+#pragma unroll 4
   for (int i = threadIdx.x; i < n / 2; i += 256)
     qr[i] = (uint32_t)float_to_half_bits(xr[2 * i] * r * w[2 * i]) |
             ((uint32_t)float_to_half_bits(xr[2 * i + 1] * r * w[2 * i + 1]) << 16);
