@@ -576,6 +576,19 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_ks(const uint32_t* __restrict_
     yres = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         y_rsrc, threadIdx.x < kRows && o < n_out ? (uint32_t)o * 4 : kOOB, 0, 0));
   }
+  // K split over the waves (KS > 1): x (and the norm weights) are taken by an empty statement here, after the
+  // weights are requested. Left alone, the compiler sinks their loads into the staging branch below, behind the
+  // weights', and the staging's wait for x then waits for the weights too; here the wait is for x alone (vector memory
+  // completes in order). Measured: the 2048 x 8192 down projection 5.06 -> 4.94 us; with KS = 1 (C0, the decode
+  // gate|up) the same pin was slower (4.31 -> 4.45 and 6.31 -> 6.79 us), so those keep the compiler's order.
+  if constexpr (KS > 1) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+      asm volatile("" ::"v"(xa[i].x), "v"(xa[i].y), "v"(xa[i].z), "v"(xa[i].w), "v"(xc[i].x), "v"(xc[i].y),
+                   "v"(xc[i].z), "v"(xc[i].w));
+      if constexpr (NORM) asm volatile("" ::"v"(xn[i].x), "v"(xn[i].y), "v"(xn[i].z), "v"(xn[i].w));
+    }
+  }
   // K % 32 == 0, so kw % 4 == 0: whole quads stage together, as stage_digits needs. With a norm, x * norm_w is
   // staged and sum(x^2) gathered; the sums are scaled by 1 / sqrt(mean(x^2) + eps) at the end (RMSNorm).
   float ss = 0.f;
